@@ -1,0 +1,218 @@
+#!/usr/bin/env python3
+"""SR-BCRS 16x8 fp32 SpMM benchmark on one MI355X.
+
+One "step" = one C = A * B over the whole workload (all launches of the
+chosen schedule) with A (converted), B and C resident in HBM.  Conversion is
+outside the timed region (the reference's kernel_only_post_conversion
+contract).  Prints ONE JSON line.
+
+Default workload: uniform-65536 at N = 512 (the metric's configuration).
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, published
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix, published
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="uniform-65536",
+                    choices=["uniform-4096", "uniform-65536", "banded-524288", "rmat-2^20", "gcn-232965"])
+    ap.add_argument("--N", type=int, default=None, help="dense width (default: the workload's)")
+    ap.add_argument("--schedule", default="auto", help="row | split[:cap] | strict_lb[:w] | multi_bind | auto")
+    ap.add_argument("--kernel", default="srbcrs", choices=["srbcrs", "csr"])
+    ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline leg")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-check", action="store_true")
+    return ap.parse_args()
+
+
+def algorithmic_bytes(M, N, Mo, nb, nnz, kernel):
+    """Dataflow bytes per launch.  SR-BCRS: metadata + A blocks + B rows
+    gathered per block + C written.  CSR: rowptr + (col, val) + B row per
+    nonzero + C."""
+    if kernel == "srbcrs":
+        return 4 * (Mo + 1) + nb * (8 * 4 + 128 * 4) + nb * 8 * N * 4 + M * N * 4
+    return 4 * (M + 1) + 8 * nnz + 4 * N * nnz + 4 * M * N
+
+
+def main():
+    args = parse()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print(json.dumps({"error": "this benchmark measures one GPU; --gpus must be 1 "
+                                   "(the SpMM path is single-GPU, sharding is design-only)"}))
+        sys.exit(2)
+
+    import torch
+    from mask_amd import datasets
+    from mask_amd.SRBCRSSpMM import Plan, csr_spmm
+
+    dev = torch.device("cuda", 0)
+    t0 = time.time()
+    m = datasets.make_config(args.config)
+    N = args.N or m.N
+    B_host = m.dense(N)
+    print(f"[bench] workload {m.name} M={m.M} K={m.K} nnz={m.nnz} N={N} gen {time.time() - t0:.1f}s",
+          file=sys.stderr, flush=True)
+
+    rowptr_d = torch.from_numpy(m.rowptr).to(dev)
+    colind_d = torch.from_numpy(m.colind).to(dev)
+    values_d = torch.from_numpy(m.values).to(dev)
+    B = torch.from_numpy(B_host).to(dev)
+    C = torch.empty((m.M, N), dtype=torch.float32, device=dev)
+
+    t0 = time.time()
+    plan = Plan(rowptr_d, colind_d, values_d, m.M)
+    conv_s = time.time() - t0
+    nb, Mo = plan.total_blocks, plan.row_windows
+    sched = args.schedule
+    if sched == "auto":
+        lens = np.diff(np.asarray(datasets_soff(plan)))
+        sched = "split" if lens.size and lens.max() > max(64, 4 * max(1, int(np.percentile(lens, 95)))) else "row"
+    name, _, param = sched.partition(":")
+    plan.set_schedule(name, int(param) if param else 0)
+    max_col = plan.max_col
+
+    if args.kernel == "srbcrs":
+        step = lambda: plan.run(B, C)
+    else:
+        step = lambda: csr_spmm(rowptr_d, colind_d, values_d, B, m.M, max_col=max_col, out=C)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    torch.cuda.synchronize()
+    t_wall = time.perf_counter()
+    evs[0].record(stream)
+    for i in range(args.steps):
+        step()
+        evs[i + 1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    per = np.array([evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps)])  # ms
+    total_ms = evs[0].elapsed_time(evs[-1])
+    ms_step = total_ms / args.steps
+    t_s = ms_step / 1e3
+    flops = 2.0 * m.nnz * N
+    gflops = flops / t_s / 1e9
+
+    ab = algorithmic_bytes(m.M, N, Mo, nb, m.nnz, args.kernel)
+    compulsory = (nb * (8 * 4 + 128 * 4) + 4 * (Mo + 1) if args.kernel == "srbcrs" else 8 * m.nnz) \
+        + m.K * N * 4 + m.M * N * 4
+    achieved = ab / t_s / 1e9
+    padded_flops = 2.0 * 128 * nb * N
+
+    result = {
+        "metric": "SpMM GFLOP/s at N=512 fp32 on 1 MI355X; % of HBM roofline",
+        "value": round(gflops, 2),
+        "unit": "GFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "ms_per_step_median": round(float(np.median(per)), 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (seeded numpy, see mask_amd/datasets.py)",
+        "config": {"workload": m.name, "M": m.M, "K": m.K, "N": N, "nnz": m.nnz, "blocks": nb,
+                   "block_fill": round(m.nnz / (128 * max(nb, 1)), 4), "kernel": args.kernel,
+                   "schedule": f"{plan.policy[0]}:{plan.policy[1]}", "seed": m.seed,
+                   "conversion_s": round(conv_s, 3), "meta": m.meta},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "algorithmic_bytes": int(ab), "compulsory_bytes": int(compulsory),
+                     "compulsory_frac": round(compulsory / t_s / 1e9 / HBM_PEAK_GBS, 4),
+                     "mfma_padded_tflops": round(padded_flops / t_s / 1e12, 3),
+                     "mfma_frac": round(padded_flops / t_s / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)},
+        "wall_s_timed": round(wall, 4),
+    }
+
+    if not args.no_check:
+        result["parity"] = check_sample(m, B_host, C.cpu().numpy(), N)
+
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(m, B_host, N, args.cpu_seconds)
+
+    print(json.dumps(result), flush=True)
+
+
+def datasets_soff(plan):
+    import torch
+    n = plan.row_windows + 1
+    t = torch.empty(n, dtype=torch.int32, device=plan.device)
+    from mask_amd import _capi
+    _capi.check(_capi.lib().srbcrs_plan_export_index(plan.handle, t.data_ptr(), n, None, 0,
+                                                     torch.cuda.current_stream(plan.device).cuda_stream))
+    return t.cpu().numpy()
+
+
+def _row_sample(m, rows):
+    rp = m.rowptr
+    counts = rp[rows + 1] - rp[rows]
+    sub_rp = np.zeros(rows.size + 1, np.int64)
+    sub_rp[1:] = np.cumsum(counts)
+    idx = np.concatenate([np.arange(rp[r], rp[r + 1]) for r in rows]) if rows.size else np.zeros(0, np.int64)
+    return sub_rp.astype(np.int32), m.colind[idx], m.values[idx]
+
+
+def check_sample(m, B_host, C, N, n_rows=4096):
+    """Correctness gate on a seeded row sample against the fp64 oracle."""
+    from oracle import oracle
+    rng = np.random.default_rng(0)
+    rows = np.sort(rng.choice(m.M, size=min(n_rows, m.M), replace=False))
+    rp, ci, vv = _row_sample(m, rows)
+    C64, absAB = oracle.csr_spmm_f64(rp, ci, vv, B_host, rows.size, with_abs=True)
+    met = oracle.error_metrics(C[rows], C64, absAB)
+    met["rows_checked"] = int(rows.size)
+    met["pass"] = bool(met["finite"] and met["max_ratio"] <= 1e-4 and met["ref_gate"])
+    return met
+
+
+def cpu_baseline(m, B_host, N, budget_s):
+    """The oracle's fp32 CSR SpMM (csr_spmm_value_kernel's arithmetic) on the
+    host cores over a bounded row sample, repeated within the time budget."""
+    from oracle import oracle
+    cores = len(os.sched_getaffinity(0))
+    # sample sized for ~1 s per repetition at ~1 GFLOP/s per core
+    target_flops = 1e9 * cores
+    rows_needed = int(target_flops / max(1.0, 2.0 * N * m.nnz / m.M))
+    rows = np.arange(min(m.M, max(16, rows_needed)))
+    rp, ci, vv = _row_sample(m, rows)
+    oracle.csr_spmm_f32(rp, ci, vv, B_host, rows.size, nthreads=cores)  # warmup
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t = time.perf_counter()
+        oracle.csr_spmm_f32(rp, ci, vv, B_host, rows.size, nthreads=cores)
+        times.append(time.perf_counter() - t)
+        if len(times) >= 200:
+            break
+    t_med = float(np.median(times))
+    nnz_s = int(rp[-1])
+    return {"value": round(2.0 * nnz_s * N / t_med / 1e9, 3), "unit": "GFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"first {rows.size} rows ({nnz_s} nnz) of {m.name} at N={N}, median of {len(times)} runs, "
+                      f"fp32 row-parallel CSR (oracle/srbcrs_oracle.c)",
+            "median_s": round(t_med, 5)}
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,148 @@
+/*
+ * srbcrs.h -- C ABI of the MI355X (gfx950) SR-BCRS SpMM backend.
+ *
+ * Plain pointers and sizes only.  Every function returns SRBCRS_OK (0) or a
+ * negative status; srbcrs_last_error() then holds a message for the calling
+ * thread.  "d_" pointers are device (HBM) pointers, others host pointers.
+ * `stream` is a hipStream_t (NULL = the null stream).
+ *
+ * Reference interfaces replaced (paths relative to the reference root):
+ *   SRK = examples/src_fp32/sr_bcrs/testbed/SRBCRSSpMM_kernel.cu
+ *   SRC = examples/src_fp32/sr_bcrs/testbed/SRBCRSSpMM.cpp
+ *   CFE = examples/src_fp32/acc/testbed/custom_format_e2e.cu
+ */
+#ifndef MASK_AMD_SRBCRS_H
+#define MASK_AMD_SRBCRS_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SRBCRS_OK 0
+#define SRBCRS_EINVAL (-1)   /* bad argument (the reference's TORCH_CHECK failures) */
+#define SRBCRS_EHIP (-2)     /* HIP runtime error */
+#define SRBCRS_ENOMEM (-3)   /* allocation failed */
+#define SRBCRS_ESTATE (-4)   /* wrong object state (e.g. run on another device) */
+
+typedef struct srbcrs_plan srbcrs_plan;
+typedef struct srbcrs_schedule srbcrs_schedule;
+
+/* Message of the last failing call on this thread ("" if none). */
+const char *srbcrs_last_error(void);
+
+/* Library version string. */
+const char *srbcrs_version(void);
+
+/* ---- Host conversion CSR -> SR-BCRS (bit-exact with SRK:226-282 for 16x8
+ * and SRK:284-340 for 32x32; the per-window block count and the padding /
+ * swizzle / last-write-wins rules of preprocess_gpu_srcfp32_srbcrs).
+ * Two calls: count fills soff[Mo+1] (Mo = ceil(num_nodes/blk_h)) and the
+ * total block count; fill writes sidx[blk_w*total], val[blk_h*blk_w*total]
+ * and, when non-NULL, block_partition[Mo], edge_to_row[nnz],
+ * edge_to_col[nnz] (entries of edges outside rows [0, num_nodes) untouched).
+ * (blk_h, blk_w) must be (16, 8) or (32, 32). */
+int srbcrs_convert_count(const int32_t *rowptr, const int32_t *colind, int32_t num_nodes,
+                         int64_t nnz, int32_t blk_h, int32_t blk_w, int32_t *soff,
+                         int64_t *total_blocks);
+int srbcrs_convert_fill(const int32_t *rowptr, const int32_t *colind, const float *values,
+                        int32_t num_nodes, int64_t nnz, int32_t blk_h, int32_t blk_w,
+                        const int32_t *soff, int32_t *sidx, float *val, int32_t *block_partition,
+                        int32_t *edge_to_row, int32_t *edge_to_col);
+
+/* ---- Plans: the device-resident SR-BCRS matrix.  Replaces the reference's
+ * preprocess_gpu_srcfp32_srbcrs + its process-global CacheEntry
+ * (SRK:27-45, SRK:172-393; pybind preprocess_gpu_16x8 / preprocess_gpu at
+ * SRC:77-118).  Inputs are CSR arrays on the device (is_device = 1, copied
+ * to the host for conversion as the reference does) or on the host.  On
+ * success *out owns device copies of soff / sidx / val on the current
+ * device. */
+int srbcrs_plan_create(const int32_t *rowptr, const int32_t *colind, const float *values,
+                       int32_t num_nodes, int64_t nnz, int32_t blk_h, int32_t blk_w,
+                       int32_t is_device, void *stream, srbcrs_plan **out);
+void srbcrs_plan_destroy(srbcrs_plan *plan);
+
+/* Plan metadata.  d_soff / d_sidx / d_val are owned by the plan. */
+typedef struct srbcrs_plan_desc {
+  int32_t num_nodes;
+  int32_t blk_h, blk_w;
+  int32_t row_windows;    /* Mo */
+  int32_t max_col;        /* largest column index in the CSR, -1 if nnz == 0 */
+  int32_t device;
+  int64_t nnz;
+  int64_t total_blocks;
+  const int32_t *d_soff;  /* row_window_offset, Mo + 1 */
+  const int32_t *d_sidx;  /* tcblocktile_id, blk_w * total_blocks */
+  const float *d_val;     /* swizzled block values, blk_h * blk_w * total_blocks */
+} srbcrs_plan_desc;
+int srbcrs_plan_get(const srbcrs_plan *plan, srbcrs_plan_desc *out);
+
+/* Write block_partition[Mo], edge_to_col[nnz] and edge_to_row[nnz] (device
+ * buffers) as preprocess does, each only when its buffer length is at least
+ * the needed size (SRK:355-366).  NULL / short buffers are skipped. */
+int srbcrs_plan_write_edges(const srbcrs_plan *plan, int32_t *d_block_partition,
+                            int64_t block_partition_len, int32_t *d_edge_to_col,
+                            int64_t edge_to_col_len, int32_t *d_edge_to_row,
+                            int64_t edge_to_row_len, void *stream);
+
+/* Copy the plan's row_window_offset (Mo + 1) and tcblocktile_id
+ * (blk_w * total_blocks) into caller-owned device buffers: the first and
+ * third members of preprocess's result tuple (SRK:343-392).  A NULL buffer
+ * is skipped; a short one is an error. */
+int srbcrs_plan_export_index(const srbcrs_plan *plan, int32_t *d_row_window_offset,
+                             int64_t row_window_offset_len, int32_t *d_tcblocktile_id,
+                             int64_t tcblocktile_id_len, void *stream);
+
+/* ---- Execution schedules (host logic).  policy:
+ *   "row"        one task per row window, written straight into C
+ *                (the plain kernel's mapping, kernel.inc:1590-1700);
+ *   "split"      row windows cut into segments of at most `param` blocks
+ *                (0 = automatic p95 / heavy-tail rule of CFE:640-699);
+ *   "strict_lb"  fixed-work groups of `param` blocks (0 = 64), the
+ *                fragmenting of strict_load_balance
+ *                (main_strict_lb_16x8.cu:208-256, CFE:719-749);
+ *   "multi_bind" windows above 2x the mean split into ceil(x/mean) parts
+ *                (main_multi_bind_16x8.cu:211-270, CFE:750-780).
+ * Partial windows go to private partial tiles that a deterministic segment
+ * reduction (fixed slot order) sums into C: no atomics anywhere, unlike
+ * the reference's atomicAdd edges (kernel_lb.inc:9-58).
+ * Export arrays (host) sized from srbcrs_schedule_info:
+ *   group_off[n_groups+1], task_begin/end/window/slot[n_tasks]
+ *   (slot -1 = direct store), red_window[n_red], red_slot_off[n_red+1]. */
+int srbcrs_schedule_build(const int32_t *soff, int32_t row_windows, const char *policy,
+                          int32_t param, srbcrs_schedule **out);
+int srbcrs_schedule_info(const srbcrs_schedule *s, int32_t *n_groups, int32_t *n_tasks,
+                         int32_t *n_slots, int32_t *n_red);
+int srbcrs_schedule_export(const srbcrs_schedule *s, int32_t *group_off, int32_t *task_begin,
+                           int32_t *task_end, int32_t *task_window, int32_t *task_slot,
+                           int32_t *red_window, int32_t *red_slot_off);
+void srbcrs_schedule_destroy(srbcrs_schedule *s);
+
+/* Select the schedule a plan runs with (default "row").  Uploads the task
+ * tables to the plan's device. */
+int srbcrs_plan_set_schedule(srbcrs_plan *plan, const char *policy, int32_t param);
+
+/* ---- SpMM.  C[0:c_rows, 0:N] = A * B with A the plan's matrix
+ * (replaces run_spmm_srcfp32_srbcrs, SRK:395-557, pybind run_SRBCRS_16x8 /
+ * run_SRBCRS and the *_balance aliases, SRC:120-192).  B is K x N
+ * row-major with leading dimension ldb, C is c_rows x N with ldc.
+ * Requirements: 16 x 8 plan, N % 16 == 0, K > max column, c_rows >=
+ * num_nodes (rows beyond num_nodes are not written).  Every row
+ * < num_nodes of C is overwritten (zeros for empty windows).  Schedules
+ * other than "row" use a plan-owned partial buffer grown on demand. */
+int srbcrs_run(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int64_t ldb,
+               float *d_C, int64_t ldc, int64_t c_rows, void *stream);
+
+/* ---- CSR fallback for low block density: C[r, :] = sum_e val[e] *
+ * B[col[e], :], fp32, edge order.  The arithmetic of csr_spmm_value_kernel
+ * (SRK:66-105), one wave64 per row.  max_col (host-known bound on colind,
+ * -1 if unknown) is checked against K. */
+int srbcrs_csr_spmm(const int32_t *d_rowptr, const int32_t *d_colind, const float *d_values,
+                    int32_t M, int64_t nnz, int32_t max_col, const float *d_B, int64_t K,
+                    int64_t N, int64_t ldb, float *d_C, int64_t ldc, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MASK_AMD_SRBCRS_H */

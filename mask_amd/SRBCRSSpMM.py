@@ -1,0 +1,307 @@
+"""Drop-in for the reference's ``SRBCRSSpMM`` torch extension module.
+
+Same function names, argument order, return shapes and error messages as the
+pybind module (examples/src_fp32/sr_bcrs/testbed/SRBCRSSpMM.cpp:194-204 and
+SRBCRSSpMM_kernel.cu:172-557), backed by the gfx950 C ABI
+(include/srbcrs.h) through ctypes.  Torch is used only for device memory and
+the current stream.
+
+Module state mirrors the reference's process-global cache
+(SRBCRSSpMM_kernel.cu:27-45): ``preprocess_*`` creates a plan keyed by
+``row_window_offset.data_ptr()`` and ``run_*`` looks it up by the same key.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+from typing import Dict, List, Optional, Tuple
+
+import torch
+
+from . import _capi
+
+Tensor = torch.Tensor
+
+_POLICIES = ("row", "split", "strict_lb", "multi_bind")
+
+
+def _check_input(t: Tensor, name: str) -> None:
+    # CHECK_INPUT (SRBCRSSpMM.cpp:6-10)
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a CUDA tensor")
+    if not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")
+
+
+def _stream_handle(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+class Plan:
+    """A device-resident SR-BCRS matrix (owns a ``srbcrs_plan``)."""
+
+    def __init__(self, rowptr, colind, values, num_nodes: int, blk_h: int = 16, blk_w: int = 8,
+                 device: Optional[torch.device] = None):
+        L = _capi.lib()
+        on_dev = isinstance(rowptr, Tensor) and rowptr.is_cuda
+        if on_dev:
+            self.device = rowptr.device
+        elif device is None:
+            self.device = torch.device("cuda", torch.cuda.current_device())
+        else:
+            self.device = torch.device(device)
+        self._keep = (rowptr, colind, values)
+        nnz = int(colind.numel() if isinstance(colind, Tensor) else len(colind))
+        h = ctypes.c_void_p()
+        with torch.cuda.device(self.device):
+            stream = _stream_handle(self.device) if on_dev else None
+            _capi.check(L.srbcrs_plan_create(_capi.ptr(rowptr), _capi.ptr(colind), _capi.ptr(values), int(num_nodes),
+                                             nnz, int(blk_h), int(blk_w), 1 if on_dev else 0, stream,
+                                             ctypes.byref(h)))
+        self._h = h
+        d = _capi.PlanDesc()
+        _capi.check(L.srbcrs_plan_get(h, ctypes.byref(d)))
+        self.desc = d
+        self.num_nodes = int(num_nodes)
+        self.nnz = nnz
+        self.blk_h, self.blk_w = int(blk_h), int(blk_w)
+        self.row_windows = int(d.row_windows)
+        self.total_blocks = int(d.total_blocks)
+        self.max_col = int(d.max_col)
+        self.policy = ("row", 0)
+
+    @property
+    def handle(self):
+        return self._h
+
+    def set_schedule(self, policy: str = "row", param: int = 0) -> None:
+        if (policy, param) == self.policy:
+            return
+        with torch.cuda.device(self.device):
+            _capi.check(_capi.lib().srbcrs_plan_set_schedule(self._h, policy.encode(), int(param)))
+        self.policy = (policy, param)
+
+    def block_fill(self) -> float:
+        """nnz / (blocks * blk_h * blk_w): the stored-value density."""
+        return self.nnz / max(1, self.total_blocks * self.blk_h * self.blk_w)
+
+    def run(self, dense: Tensor, out: Optional[Tensor] = None) -> Tensor:
+        """out[:num_nodes] = A @ dense on the current stream."""
+        if out is None:
+            out = torch.empty((self.num_nodes, dense.shape[1]), dtype=torch.float32, device=dense.device)
+        with torch.cuda.device(self.device):
+            _capi.check(_capi.lib().srbcrs_run(self._h, dense.data_ptr(), int(dense.shape[0]), int(dense.shape[1]),
+                                               int(dense.stride(0)), out.data_ptr(), int(out.stride(0)),
+                                               int(out.shape[0]), _stream_handle(self.device)))
+        return out
+
+    def close(self) -> None:
+        if getattr(self, "_h", None):
+            _capi.lib().srbcrs_plan_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class _Entry:
+    __slots__ = ("plan", "num_nodes", "num_edges", "use_16x8", "tensors")
+
+    def __init__(self, plan, num_nodes, num_edges, use_16x8, tensors):
+        self.plan, self.num_nodes, self.num_edges, self.use_16x8, self.tensors = (
+            plan, num_nodes, num_edges, use_16x8, tensors)
+
+
+_cache_mu = threading.Lock()
+_cache: Dict[int, _Entry] = {}
+
+
+def clear_cache() -> None:
+    with _cache_mu:
+        _cache.clear()
+
+
+def _preprocess(colind: Tensor, rowptr: Tensor, values: Tensor, num_nodes: int, blk_h: int, blk_w: int,
+                block_partition: Tensor, edge_to_col: Tensor, edge_to_row: Tensor, use_16x8: bool):
+    for t, n in ((colind, "colind"), (rowptr, "rowptr"), (values, "values"), (block_partition, "block_partition"),
+                 (edge_to_col, "edge_to_col"), (edge_to_row, "edge_to_row")):
+        _check_input(t, n)
+    if colind.dtype != torch.int32:
+        raise RuntimeError("colind must be int32")
+    if rowptr.dtype != torch.int32:
+        raise RuntimeError("rowptr must be int32")
+    if values.dtype != torch.float32:
+        raise RuntimeError("values must be float32")
+    if num_nodes < 1:
+        raise RuntimeError("num_nodes must be positive")
+    tile_m, tile_k = (16, 8) if use_16x8 else (32, 32)
+    if blk_h != tile_m:
+        raise RuntimeError(f"blk_h mismatch for SR-BCRS variant: expected {tile_m} got {blk_h}")
+    if blk_w != tile_k:
+        raise RuntimeError(f"blk_w mismatch for SR-BCRS variant: expected {tile_k} got {blk_w}")
+    nnz = int(colind.numel())
+    if values.numel() != nnz:
+        raise RuntimeError("values length must equal colind length")
+    plan = Plan(rowptr, colind, values, num_nodes, tile_m, tile_k)
+    dev = colind.device
+    total = plan.total_blocks
+    mo = plan.row_windows
+    i32 = dict(dtype=torch.int32, device=dev)
+    row_window_offset = torch.empty(mo + 1, **i32)
+    tcblocktile_id = torch.empty(total * tile_k, **i32)
+    with torch.cuda.device(dev):
+        st = _stream_handle(dev)
+        _capi.check(_capi.lib().srbcrs_plan_export_index(plan.handle, row_window_offset.data_ptr(), mo + 1,
+                                                         tcblocktile_id.data_ptr() if total else None,
+                                                         total * tile_k, st))
+        _capi.check(_capi.lib().srbcrs_plan_write_edges(plan.handle, block_partition.data_ptr(),
+                                                        block_partition.numel(), edge_to_col.data_ptr(),
+                                                        edge_to_col.numel(), edge_to_row.data_ptr(),
+                                                        edge_to_row.numel(), st))
+    tcblock_rowid = torch.zeros(total, **i32)
+    tcblock_offset = torch.zeros(1, **i32)
+    sparse_a_to_x_idx = torch.zeros(1, **i32)
+    key = int(row_window_offset.data_ptr())
+    with _cache_mu:
+        # the entry keeps row_window_offset alive so the key stays unique
+        _cache[key] = _Entry(plan, int(num_nodes), nnz, use_16x8,
+                             (rowptr, colind, values, row_window_offset, tcblocktile_id))
+    return row_window_offset, tcblock_rowid, tcblocktile_id, tcblock_offset, sparse_a_to_x_idx, total
+
+
+def _tile_b_for(n: int) -> int:
+    """SRBCRS_TILE_B handling (SRBCRSSpMM_kernel.cu:435-475): validates the
+    forced tile, else picks 64/32/16 by divisibility; 0 = none fits."""
+    env = os.environ.get("SRBCRS_TILE_B")
+    if env is not None:
+        if env in ("64", "32", "16"):
+            t = int(env)
+            if n % t != 0:
+                raise RuntimeError(f"SRBCRS_TILE_B={t} requires dense feature dim divisible by {t}, got {n}")
+            return t
+        if env != "auto":
+            raise RuntimeError(f"Invalid SRBCRS_TILE_B={env}. Supported values: auto, 64, 32, 16")
+    for t in (64, 32, 16):
+        if n % t == 0:
+            return t
+    return 0
+
+
+def _schedule_from_exeplan(exeplan: str) -> Optional[Tuple[str, int]]:
+    """The reference ignores ``exeplan``; here "policy" or "policy:param"
+    with policy in row/split/strict_lb/multi_bind selects the schedule and
+    anything else is ignored.  SPARSENE_SRBCRS_SCHEDULE is the env form."""
+    spec = (exeplan or "").strip() or os.environ.get("SPARSENE_SRBCRS_SCHEDULE", "").strip()
+    if not spec:
+        return None
+    name, _, param = spec.partition(":")
+    if name not in _POLICIES:
+        return None
+    return name, int(param) if param else 0
+
+
+def _run(dense: Tensor, row_window_offset: Tensor, tcblocktile_id: Tensor, tcblock_offset: Tensor,
+         sparse_a_to_x_idx: Tensor, num_nodes: int, num_edges: int, exeplan: str, use_16x8: bool) -> List[Tensor]:
+    for t, n in ((dense, "dense"), (row_window_offset, "row_window_offset"), (tcblocktile_id, "tcblocktile_id"),
+                 (tcblock_offset, "tcblock_offset"), (sparse_a_to_x_idx, "sparse_a_to_x_idx")):
+        _check_input(t, n)
+    if dense.dtype != torch.float32:
+        raise RuntimeError("dense must be float32")
+    if dense.dim() != 2:
+        raise RuntimeError("dense must be 2-D")
+    key = int(row_window_offset.data_ptr())
+    with _cache_mu:
+        entry = _cache.get(key)
+    if entry is None:
+        raise RuntimeError("run_SRBCRS cache miss. Call preprocess_gpu before run_SRBCRS.")
+    if num_nodes != entry.num_nodes:
+        raise RuntimeError(f"num_nodes mismatch between preprocess and run: {num_nodes} vs {entry.num_nodes}")
+    if use_16x8 != entry.use_16x8:
+        raise RuntimeError("SR-BCRS variant mismatch between preprocess and run")
+    n = int(dense.shape[1])
+    if n <= 0:
+        return [torch.zeros((entry.num_nodes, 0), dtype=dense.dtype, device=dense.device)]
+    tile_b = _tile_b_for(n)
+    if tile_b == 0:
+        raise RuntimeError(f"SR-BCRS requires dense feature dim divisible by 16/32/64, got {n}. "
+                           "Please pad feature dim before run.")
+    if entry.plan.total_blocks <= 0:
+        raise RuntimeError("SR-BCRS has empty preprocessed blocks; CSR fallback disabled.")
+    if not use_16x8:
+        raise RuntimeError("SR-BCRS 32x32 execution is not available in the gfx950 backend; "
+                           "use preprocess_gpu_16x8 / run_SRBCRS_16x8")
+    sched = _schedule_from_exeplan(exeplan)
+    entry.plan.set_schedule(*(sched or ("row", 0)))
+    out = torch.empty((entry.num_nodes, n), dtype=torch.float32, device=dense.device)
+    entry.plan.run(dense, out)
+    return [out]
+
+
+# ---- the module's functions (SRBCRSSpMM.cpp:77-192) -------------------------
+
+def preprocess_gpu(colind, rowptr, values, num_nodes, blk_h, blk_w, block_partition, edge_to_col, edge_to_row):
+    """SR-BCRS preprocess base, 32x32 blocks."""
+    return _preprocess(colind, rowptr, values, num_nodes, blk_h, blk_w, block_partition, edge_to_col,
+                       edge_to_row, False)
+
+
+def preprocess_gpu_16x8(colind, rowptr, values, num_nodes, blk_h, blk_w, block_partition, edge_to_col,
+                        edge_to_row):
+    """SR-BCRS preprocess 16x8."""
+    return _preprocess(colind, rowptr, values, num_nodes, blk_h, blk_w, block_partition, edge_to_col,
+                       edge_to_row, True)
+
+
+def run_SRBCRS(dense, row_window_offset, tcblocktile_id, tcblock_offset, sparse_a_to_x_idx, num_nodes,
+               num_edges, exeplan):
+    return _run(dense, row_window_offset, tcblocktile_id, tcblock_offset, sparse_a_to_x_idx, num_nodes,
+                num_edges, exeplan, False)
+
+
+def run_SRBCRS_balance(dense, row_window_offset, tcblocktile_id, tcblock_offset, sparse_a_to_x_idx, num_nodes,
+                       exeplan):
+    return _run(dense, row_window_offset, tcblocktile_id, tcblock_offset, sparse_a_to_x_idx, num_nodes,
+                int(sparse_a_to_x_idx.numel()), exeplan, False)
+
+
+def run_SRBCRS_16x8(dense, row_window_offset, tcblocktile_id, tcblock_offset, sparse_a_to_x_idx, num_nodes,
+                    num_edges, exeplan):
+    return _run(dense, row_window_offset, tcblocktile_id, tcblock_offset, sparse_a_to_x_idx, num_nodes,
+                num_edges, exeplan, True)
+
+
+def run_SRBCRS_16x8_balance(dense, row_window_offset, tcblocktile_id, tcblock_offset, sparse_a_to_x_idx,
+                            num_nodes, exeplan):
+    return _run(dense, row_window_offset, tcblocktile_id, tcblock_offset, sparse_a_to_x_idx, num_nodes,
+                int(sparse_a_to_x_idx.numel()), exeplan, True)
+
+
+def plan_for(row_window_offset: Tensor) -> Plan:
+    """The plan behind a preprocess result (for benchmarking / inspection)."""
+    with _cache_mu:
+        e = _cache.get(int(row_window_offset.data_ptr()))
+    if e is None:
+        raise RuntimeError("run_SRBCRS cache miss. Call preprocess_gpu before run_SRBCRS.")
+    return e.plan
+
+
+def csr_spmm(rowptr: Tensor, colind: Tensor, values: Tensor, dense: Tensor, num_rows: int,
+             max_col: Optional[int] = None, out: Optional[Tensor] = None) -> Tensor:
+    """CSR fallback kernel (csr_spmm_value_kernel, SRBCRSSpMM_kernel.cu:66-105)."""
+    for t, n in ((rowptr, "rowptr"), (colind, "colind"), (values, "values"), (dense, "dense")):
+        _check_input(t, n)
+    if max_col is None:
+        max_col = int(colind.max().item()) if colind.numel() else -1
+    n = int(dense.shape[1])
+    if out is None:
+        out = torch.empty((num_rows, n), dtype=torch.float32, device=dense.device)
+    with torch.cuda.device(dense.device):
+        _capi.check(_capi.lib().srbcrs_csr_spmm(rowptr.data_ptr(), colind.data_ptr(), values.data_ptr(), int(num_rows),
+                                                int(colind.numel()), int(max_col), dense.data_ptr(),
+                                                int(dense.shape[0]), n, int(dense.stride(0)), out.data_ptr(),
+                                                int(out.stride(0)), _stream_handle(dense.device)))
+    return out

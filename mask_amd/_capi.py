@@ -1,0 +1,165 @@
+"""ctypes binding of ``libmask_srbcrs.so`` (declarations: include/srbcrs.h).
+
+The library is built in-tree by ``mask_amd.build``.  Loading never falls back
+to anything else: a missing library raises, so a GPU run cannot silently take
+a non-HIP path.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+import numpy as np
+
+LIB_PATH = Path(__file__).resolve().parent / "libmask_srbcrs.so"
+
+SRBCRS_OK = 0
+SRBCRS_EINVAL = -1
+SRBCRS_EHIP = -2
+SRBCRS_ENOMEM = -3
+SRBCRS_ESTATE = -4
+
+# Every symbol include/srbcrs.h declares (checked by the CPU test suite).
+EXPORTS = (
+    "srbcrs_last_error", "srbcrs_version",
+    "srbcrs_convert_count", "srbcrs_convert_fill",
+    "srbcrs_plan_create", "srbcrs_plan_destroy", "srbcrs_plan_get", "srbcrs_plan_write_edges",
+    "srbcrs_plan_export_index",
+    "srbcrs_schedule_build", "srbcrs_schedule_info", "srbcrs_schedule_export", "srbcrs_schedule_destroy",
+    "srbcrs_plan_set_schedule", "srbcrs_run", "srbcrs_csr_spmm",
+)
+
+_i32p = ctypes.POINTER(ctypes.c_int32)
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_f32p = ctypes.POINTER(ctypes.c_float)
+_vp = ctypes.c_void_p
+_i32 = ctypes.c_int32
+_i64 = ctypes.c_int64
+
+
+class PlanDesc(ctypes.Structure):
+    _fields_ = [
+        ("num_nodes", ctypes.c_int32),
+        ("blk_h", ctypes.c_int32),
+        ("blk_w", ctypes.c_int32),
+        ("row_windows", ctypes.c_int32),
+        ("max_col", ctypes.c_int32),
+        ("device", ctypes.c_int32),
+        ("nnz", ctypes.c_int64),
+        ("total_blocks", ctypes.c_int64),
+        ("d_soff", ctypes.c_void_p),
+        ("d_sidx", ctypes.c_void_p),
+        ("d_val", ctypes.c_void_p),
+    ]
+
+
+class SrbcrsError(RuntimeError):
+    """A failing status from the C ABI; the message is srbcrs_last_error()."""
+
+    def __init__(self, code: int, msg: str):
+        super().__init__(msg)
+        self.code = code
+
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH.name} is not built; run `python -m mask_amd.build` (hipcc, gfx950). "
+            "There is no non-HIP fallback.")
+    L = ctypes.CDLL(str(LIB_PATH))
+    sig = {
+        "srbcrs_last_error": ([], ctypes.c_char_p),
+        "srbcrs_version": ([], ctypes.c_char_p),
+        "srbcrs_convert_count": ([_vp, _vp, _i32, _i64, _i32, _i32, _vp, _i64p], ctypes.c_int),
+        "srbcrs_convert_fill": ([_vp, _vp, _vp, _i32, _i64, _i32, _i32, _vp, _vp, _vp, _vp, _vp, _vp],
+                                ctypes.c_int),
+        "srbcrs_plan_create": ([_vp, _vp, _vp, _i32, _i64, _i32, _i32, _i32, _vp, ctypes.POINTER(_vp)],
+                               ctypes.c_int),
+        "srbcrs_plan_destroy": ([_vp], None),
+        "srbcrs_plan_get": ([_vp, ctypes.POINTER(PlanDesc)], ctypes.c_int),
+        "srbcrs_plan_write_edges": ([_vp, _vp, _i64, _vp, _i64, _vp, _i64, _vp], ctypes.c_int),
+        "srbcrs_plan_export_index": ([_vp, _vp, _i64, _vp, _i64, _vp], ctypes.c_int),
+        "srbcrs_schedule_build": ([_vp, _i32, ctypes.c_char_p, _i32, ctypes.POINTER(_vp)], ctypes.c_int),
+        "srbcrs_schedule_info": ([_vp, _i32p, _i32p, _i32p, _i32p], ctypes.c_int),
+        "srbcrs_schedule_export": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp], ctypes.c_int),
+        "srbcrs_schedule_destroy": ([_vp], None),
+        "srbcrs_plan_set_schedule": ([_vp, ctypes.c_char_p, _i32], ctypes.c_int),
+        "srbcrs_run": ([_vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp], ctypes.c_int),
+        "srbcrs_csr_spmm": ([_vp, _vp, _vp, _i32, _i64, _i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp],
+                            ctypes.c_int),
+    }
+    for name, (args, res) in sig.items():
+        f = getattr(L, name)
+        f.argtypes = args
+        f.restype = res
+    _lib = L
+    return L
+
+
+def check(code: int) -> None:
+    if code != SRBCRS_OK:
+        msg = lib().srbcrs_last_error().decode(errors="replace")
+        raise SrbcrsError(code, msg)
+
+
+def ptr(a) -> int:
+    """Raw address of a numpy array or torch tensor (None -> NULL)."""
+    if a is None:
+        return None
+    if isinstance(a, np.ndarray):
+        return a.ctypes.data
+    return a.data_ptr()
+
+
+# ---- host helpers (no GPU involved) ---------------------------------------
+
+def convert_host(rowptr, colind, values, num_nodes: int, blk_h: int = 16, blk_w: int = 8) -> dict:
+    """CSR -> SR-BCRS on the host through the library's converter."""
+    L = lib()
+    rowptr = np.ascontiguousarray(rowptr, dtype=np.int32)
+    colind = np.ascontiguousarray(colind, dtype=np.int32)
+    values = np.ascontiguousarray(values, dtype=np.float32)
+    nnz = int(colind.shape[0])
+    mo = (num_nodes + blk_h - 1) // blk_h
+    soff = np.zeros(mo + 1, dtype=np.int32)
+    total = ctypes.c_int64(0)
+    check(L.srbcrs_convert_count(ptr(rowptr), ptr(colind), num_nodes, nnz, blk_h, blk_w, ptr(soff),
+                                 ctypes.byref(total)))
+    t = int(total.value)
+    sidx = np.zeros(max(t * blk_w, 1), dtype=np.int32)
+    val = np.zeros(max(t * blk_h * blk_w, 1), dtype=np.float32)
+    bp = np.zeros(max(mo, 1), dtype=np.int32)
+    e2r = np.zeros(max(nnz, 1), dtype=np.int32)
+    e2c = np.zeros(max(nnz, 1), dtype=np.int32)
+    check(L.srbcrs_convert_fill(ptr(rowptr), ptr(colind), ptr(values), num_nodes, nnz, blk_h, blk_w, ptr(soff),
+                                ptr(sidx), ptr(val), ptr(bp), ptr(e2r), ptr(e2c)))
+    return dict(soff=soff, sidx=sidx[: t * blk_w], val=val[: t * blk_h * blk_w], block_partition=bp[:mo],
+                edge_to_row=e2r[:nnz], edge_to_col=e2c[:nnz], total=t)
+
+
+def build_schedule(soff, policy: str, param: int = 0) -> dict:
+    """Host schedule tables (see srbcrs_schedule_build in include/srbcrs.h)."""
+    L = lib()
+    soff = np.ascontiguousarray(soff, dtype=np.int32)
+    h = ctypes.c_void_p()
+    check(L.srbcrs_schedule_build(ptr(soff), soff.shape[0] - 1, policy.encode(), int(param), ctypes.byref(h)))
+    try:
+        ng, nt, ns, nr = (ctypes.c_int32() for _ in range(4))
+        check(L.srbcrs_schedule_info(h, ctypes.byref(ng), ctypes.byref(nt), ctypes.byref(ns), ctypes.byref(nr)))
+        out = dict(group_off=np.zeros(ng.value + 1, np.int32), task_begin=np.zeros(nt.value, np.int32),
+                   task_end=np.zeros(nt.value, np.int32), task_window=np.zeros(nt.value, np.int32),
+                   task_slot=np.zeros(nt.value, np.int32), red_window=np.zeros(nr.value, np.int32),
+                   red_slot_off=np.zeros(nr.value + 1, np.int32))
+        check(L.srbcrs_schedule_export(h, *(ptr(out[k]) for k in ("group_off", "task_begin", "task_end",
+                                                                   "task_window", "task_slot", "red_window",
+                                                                   "red_slot_off"))))
+        out["n_slots"] = ns.value
+        return out
+    finally:
+        L.srbcrs_schedule_destroy(h)

@@ -1,0 +1,721 @@
+// C ABI of the SR-BCRS backend: host conversion, schedules, plans, launch.
+// Declarations and the reference interfaces they replace: include/srbcrs.h.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <exception>
+#include <new>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "../../include/srbcrs.h"
+#include "srbcrs_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+struct Error {
+  int code;
+  std::string msg;
+};
+
+[[noreturn]] void fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  throw Error{code, buf};
+}
+
+void hip_check(hipError_t e, const char* what) {
+  if (e != hipSuccess) fail(SRBCRS_EHIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+template <class F>
+int guarded(F&& f) {
+  try {
+    f();
+    g_last_error.clear();
+    return SRBCRS_OK;
+  } catch (const Error& e) {
+    g_last_error = e.msg;
+    return e.code;
+  } catch (const std::bad_alloc&) {
+    g_last_error = "host allocation failed";
+    return SRBCRS_ENOMEM;
+  } catch (const std::exception& e) {
+    g_last_error = e.what();
+    return SRBCRS_EINVAL;
+  }
+}
+
+// Run body(lo, hi) over [0, n) on up to hardware_concurrency threads.
+template <class F>
+void parallel_for(int64_t n, F&& body) {
+  unsigned hw = std::thread::hardware_concurrency();
+  int64_t nt = hw ? hw : 1;
+  if (nt > 64) nt = 64;
+  if (n < 4096 || nt == 1) {
+    body((int64_t)0, n);
+    return;
+  }
+  // dynamic chunks so skewed windows (power-law rows) balance
+  const int64_t chunk = std::max<int64_t>(256, n / (nt * 16));
+  std::atomic<int64_t> next{0};
+  std::vector<std::thread> th;
+  std::exception_ptr err;
+  std::atomic<bool> has_err{false};
+  for (int64_t t = 0; t < nt; ++t) {
+    th.emplace_back([&] {
+      try {
+        for (;;) {
+          int64_t lo = next.fetch_add(chunk);
+          if (lo >= n) break;
+          body(lo, std::min(n, lo + chunk));
+        }
+      } catch (...) {
+        bool expected = false;
+        if (has_err.compare_exchange_strong(expected, true)) err = std::current_exception();
+      }
+    });
+  }
+  for (auto& t : th) t.join();
+  if (err) std::rethrow_exception(err);
+}
+
+inline int swizzle_2_2_3(int o) { return o ^ ((o & 0x60) >> 3); }
+
+void check_block_shape(int blk_h, int blk_w) {
+  if (!((blk_h == 16 && blk_w == 8) || (blk_h == 32 && blk_w == 32)))
+    fail(SRBCRS_EINVAL, "unsupported SR-BCRS block %dx%d: expected 16x8 or 32x32", blk_h, blk_w);
+}
+
+void check_csr(const int32_t* rowptr, const int32_t* colind, int32_t num_nodes, int64_t nnz) {
+  if (num_nodes < 1) fail(SRBCRS_EINVAL, "num_nodes must be positive");
+  if (nnz < 0 || nnz > INT32_MAX) fail(SRBCRS_EINVAL, "nnz out of range: %lld", (long long)nnz);
+  if (!rowptr) fail(SRBCRS_EINVAL, "rowptr is NULL");
+  if (nnz > 0 && !colind) fail(SRBCRS_EINVAL, "colind is NULL");
+  if (rowptr[0] < 0) fail(SRBCRS_EINVAL, "rowptr[0] must be >= 0");
+  for (int64_t r = 0; r < num_nodes; ++r)
+    if (rowptr[r + 1] < rowptr[r])
+      fail(SRBCRS_EINVAL, "rowptr must be non-decreasing (row %lld)", (long long)r);
+  if ((int64_t)rowptr[num_nodes] > nnz)
+    fail(SRBCRS_EINVAL, "rowptr[num_nodes]=%d exceeds colind length %lld", rowptr[num_nodes],
+         (long long)nnz);
+}
+
+// Per-window sorted unique columns, stored in a scratch array at the
+// window's edge offset (a window never has more unique columns than edges).
+struct Uniq {
+  std::vector<int32_t> cols;   // size = edges covered
+  std::vector<int32_t> count;  // per window
+  int32_t max_col = -1;
+  int64_t base = 0;            // rowptr[0]
+};
+
+void build_uniq(const int32_t* rowptr, const int32_t* colind, int32_t num_nodes, int blk_h,
+                Uniq& u) {
+  const int32_t Mo = (num_nodes + blk_h - 1) / blk_h;
+  u.base = rowptr[0];
+  u.cols.assign((size_t)(rowptr[num_nodes] - rowptr[0]), 0);
+  u.count.assign((size_t)Mo, 0);
+  std::atomic<int32_t> gmax{-1};
+  std::atomic<bool> neg{false};
+  parallel_for(Mo, [&](int64_t lo, int64_t hi) {
+    int32_t lmax = -1;
+    for (int64_t w = lo; w < hi; ++w) {
+      const int64_t r0 = w * blk_h;
+      const int64_t r1 = std::min<int64_t>(r0 + blk_h, num_nodes);
+      const int64_t e0 = rowptr[r0], e1 = rowptr[r1];
+      int32_t* out = u.cols.data() + (e0 - u.base);
+      std::copy(colind + e0, colind + e1, out);
+      std::sort(out, out + (e1 - e0));
+      int32_t* end = std::unique(out, out + (e1 - e0));
+      u.count[w] = (int32_t)(end - out);
+      if (end != out) {
+        if (out[0] < 0) neg = true;
+        lmax = std::max(lmax, end[-1]);
+      }
+    }
+    int32_t cur = gmax.load();
+    while (lmax > cur && !gmax.compare_exchange_weak(cur, lmax)) {
+    }
+  });
+  if (neg) fail(SRBCRS_EINVAL, "colind holds a negative column index");
+  u.max_col = gmax.load();
+}
+
+int64_t soff_from_uniq(const Uniq& u, int blk_w, int32_t* soff) {
+  int64_t total = 0;
+  const int64_t Mo = (int64_t)u.count.size();
+  for (int64_t w = 0; w < Mo; ++w) {
+    if (total > INT32_MAX) fail(SRBCRS_EINVAL, "block count exceeds int32 offsets");
+    soff[w] = (int32_t)total;
+    total += (u.count[w] + blk_w - 1) / blk_w;
+  }
+  if (total > INT32_MAX) fail(SRBCRS_EINVAL, "block count exceeds int32 offsets");
+  soff[Mo] = (int32_t)total;
+  return total;
+}
+
+void fill_from_uniq(const int32_t* rowptr, const int32_t* colind, const float* values,
+                    int32_t num_nodes, int blk_h, int blk_w, const Uniq& u, const int32_t* soff,
+                    int32_t* sidx, float* val, int32_t* block_partition, int32_t* edge_to_row,
+                    int32_t* edge_to_col) {
+  const int32_t Mo = (num_nodes + blk_h - 1) / blk_h;
+  const int64_t bsz = (int64_t)blk_h * blk_w;
+  parallel_for(Mo, [&](int64_t lo, int64_t hi) {
+    for (int64_t w = lo; w < hi; ++w) {
+      const int32_t cnt = u.count[w];
+      const int32_t nb = (cnt + blk_w - 1) / blk_w;
+      if (soff[w + 1] - soff[w] != nb) fail(SRBCRS_EINVAL, "soff does not match the CSR (window %lld)", (long long)w);
+      if (block_partition) block_partition[w] = nb;
+      const int64_t r0 = w * blk_h;
+      const int64_t r1 = std::min<int64_t>(r0 + blk_h, num_nodes);
+      const int32_t* cols = u.cols.data() + (rowptr[r0] - u.base);
+      int32_t* sw = sidx + (int64_t)soff[w] * blk_w;
+      for (int64_t i = 0; i < (int64_t)nb * blk_w; ++i) sw[i] = i < cnt ? cols[i] : cols[cnt - 1];
+      float* vw = val + (int64_t)soff[w] * bsz;
+      std::fill(vw, vw + nb * bsz, 0.0f);
+      for (int64_t r = r0; r < r1; ++r) {
+        const int ir = (int)(r - r0);
+        for (int64_t e = rowptr[r]; e < rowptr[r + 1]; ++e) {
+          const int32_t c = colind[e];
+          const int32_t pos = (int32_t)(std::lower_bound(cols, cols + cnt, c) - cols);
+          if (edge_to_row) edge_to_row[e] = (int32_t)r;
+          if (edge_to_col) edge_to_col[e] = pos;
+          const int o = ir * blk_w + pos % blk_w;
+          vw[(int64_t)(pos / blk_w) * bsz + swizzle_2_2_3(o)] = values[e];
+        }
+      }
+    }
+  });
+}
+
+// ---- schedules ------------------------------------------------------------
+
+struct Schedule {
+  std::string policy;
+  int32_t param = 0;
+  std::vector<int32_t> group_off{0};
+  std::vector<int32_t> task_begin, task_end, task_window, task_slot;
+  std::vector<int32_t> red_window, red_slot_off{0};
+  int32_t n_slots = 0;
+};
+
+// Give every task of a window with several tasks its own partial slot (in
+// task order) and list those windows, plus windows without any task, for
+// the reduction.  Windows with one task store directly.
+void assign_slots(Schedule& s, int32_t Mo) {
+  std::vector<int32_t> ntask(Mo, 0);
+  for (int32_t w : s.task_window) ntask[w]++;
+  std::vector<int32_t> first_slot(Mo, -1);
+  // slots of one window must be contiguous: allocate in window order
+  int32_t next = 0;
+  for (int32_t w = 0; w < Mo; ++w) {
+    if (ntask[w] >= 2) {
+      first_slot[w] = next;
+      next += ntask[w];
+    }
+  }
+  std::vector<int32_t> seen(Mo, 0);
+  for (size_t t = 0; t < s.task_window.size(); ++t) {
+    const int32_t w = s.task_window[t];
+    s.task_slot[t] = ntask[w] >= 2 ? first_slot[w] + seen[w]++ : -1;
+  }
+  for (int32_t w = 0; w < Mo; ++w) {
+    if (ntask[w] == 0 || ntask[w] >= 2) {
+      s.red_window.push_back(w);
+      s.red_slot_off.push_back(s.red_slot_off.back() + (ntask[w] >= 2 ? ntask[w] : 0));
+    }
+  }
+  s.n_slots = next;
+}
+
+void push_task(Schedule& s, int32_t b, int32_t e, int32_t w) {
+  s.task_begin.push_back(b);
+  s.task_end.push_back(e);
+  s.task_window.push_back(w);
+  s.task_slot.push_back(-1);
+}
+
+Schedule* build_schedule(const int32_t* soff, int32_t Mo, const char* policy_c, int32_t param) {
+  if (!soff) fail(SRBCRS_EINVAL, "soff is NULL");
+  if (Mo < 0) fail(SRBCRS_EINVAL, "row_windows must be >= 0");
+  for (int32_t w = 0; w < Mo; ++w)
+    if (soff[w + 1] < soff[w]) fail(SRBCRS_EINVAL, "soff must be non-decreasing");
+  std::string policy = policy_c ? policy_c : "row";
+  if (policy.empty()) policy = "row";
+  if (param < 0) fail(SRBCRS_EINVAL, "schedule parameter must be >= 0");
+  auto* s = new Schedule();
+  s->policy = policy;
+  s->param = param;
+  try {
+    if (policy == "row") {
+      for (int32_t w = 0; w < Mo; ++w) {
+        push_task(*s, soff[w], soff[w + 1], w);
+        s->group_off.push_back((int32_t)s->task_begin.size());
+      }
+    } else if (policy == "split") {
+      // custom_format_e2e.cu:640-699: p95 / heavy-tail cap, then segments
+      int32_t cap;
+      if (param > 0) {
+        cap = param;
+      } else {
+        std::vector<int32_t> len(Mo);
+        int32_t mx = 0;
+        for (int32_t w = 0; w < Mo; ++w) {
+          len[w] = soff[w + 1] - soff[w];
+          mx = std::max(mx, len[w]);
+        }
+        int32_t p95 = 0;
+        if (Mo > 0) {
+          std::sort(len.begin(), len.end());
+          int64_t i = (int64_t)std::ceil(Mo * 0.95) - 1;
+          i = std::min<int64_t>(std::max<int64_t>(i, 0), Mo - 1);
+          p95 = len[i];
+        }
+        const int32_t p = std::max(p95, 1);
+        const bool heavy = mx > std::max(64, 4 * p);
+        cap = heavy ? std::max(32, std::min(128, 2 * p95)) : std::max(mx, 1);
+      }
+      s->param = cap;
+      for (int32_t w = 0; w < Mo; ++w) {
+        const int32_t b = soff[w], e = soff[w + 1];
+        if (b == e) {
+          push_task(*s, b, e, w);
+          s->group_off.push_back((int32_t)s->task_begin.size());
+        }
+        for (int64_t t = b; t < e; t += cap) {
+          push_task(*s, (int32_t)t, (int32_t)std::min<int64_t>(t + cap, e), w);
+          s->group_off.push_back((int32_t)s->task_begin.size());
+        }
+      }
+    } else if (policy == "strict_lb") {
+      // main_strict_lb_16x8.cu:208-256: fixed `workload` blocks per group
+      const int32_t workload = param > 0 ? param : 64;
+      s->param = workload;
+      int32_t cur = 0;
+      for (int32_t w = 0; w < Mo; ++w) {
+        int32_t b = soff[w];
+        const int32_t e = soff[w + 1];
+        while (b < e) {
+          const int32_t take = std::min(workload - cur, e - b);
+          push_task(*s, b, b + take, w);
+          b += take;
+          cur += take;
+          if (cur == workload) {
+            s->group_off.push_back((int32_t)s->task_begin.size());
+            cur = 0;
+          }
+        }
+      }
+      if (cur != 0 || s->group_off.size() == 1) s->group_off.push_back((int32_t)s->task_begin.size());
+    } else if (policy == "multi_bind") {
+      // main_multi_bind_16x8.cu:211-270: alpha = 2, parts = ceil(x / mean)
+      double avg = 0.0;
+      for (int32_t w = 0; w < Mo; ++w) avg += (double)(soff[w + 1] - soff[w]);
+      if (Mo > 0) avg /= (double)Mo;
+      for (int32_t w = 0; w < Mo; ++w) {
+        const int32_t x = soff[w + 1] - soff[w];
+        if (x == 0) continue;
+        int32_t parts = 1;
+        if (avg > 0.0 && x > 2.0 * avg) {
+          const double p = std::ceil((double)x / avg);
+          parts = p > 9999.0 ? 9999 : std::max(1, (int32_t)p);
+        }
+        const int32_t base = x / parts, rem = x % parts;
+        int32_t b = soff[w];
+        for (int32_t i = 0; i < parts; ++i) {
+          const int32_t take = base + (i < rem ? 1 : 0);
+          push_task(*s, b, b + take, w);
+          s->group_off.push_back((int32_t)s->task_begin.size());
+          b += take;
+        }
+      }
+    } else {
+      fail(SRBCRS_EINVAL, "unknown schedule policy '%s' (row, split, strict_lb, multi_bind)",
+           policy.c_str());
+    }
+    assign_slots(*s, Mo);
+  } catch (...) {
+    delete s;
+    throw;
+  }
+  return s;
+}
+
+// ---- device memory helpers ------------------------------------------------
+
+template <class T>
+T* dev_alloc(size_t n) {
+  void* p = nullptr;
+  if (n == 0) n = 1;
+  hipError_t e = hipMalloc(&p, n * sizeof(T));
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    fail(SRBCRS_ENOMEM, "hipMalloc(%zu bytes) failed: %s", n * sizeof(T), hipGetErrorString(e));
+  }
+  return static_cast<T*>(p);
+}
+
+template <class T>
+void dev_free(T*& p) {
+  if (p) (void)hipFree(p);
+  p = nullptr;
+}
+
+template <class T>
+T* upload(const std::vector<T>& v) {
+  T* d = dev_alloc<T>(v.size());
+  if (!v.empty()) hip_check(hipMemcpy(d, v.data(), v.size() * sizeof(T), hipMemcpyHostToDevice), "hipMemcpy H2D");
+  return d;
+}
+
+}  // namespace
+
+struct srbcrs_schedule {
+  Schedule s;
+};
+
+struct srbcrs_plan {
+  int device = 0;
+  int32_t num_nodes = 0, blk_h = 16, blk_w = 8, Mo = 0, max_col = -1;
+  int64_t nnz = 0, total = 0;
+  int32_t* d_soff = nullptr;
+  int32_t* d_sidx = nullptr;
+  float* d_val = nullptr;
+  std::vector<int32_t> h_soff;
+  // edge maps kept on the host until requested
+  std::vector<int32_t> h_block_partition, h_edge_to_row, h_edge_to_col;
+  // schedule
+  Schedule sched;
+  int32_t *d_group_off = nullptr, *d_task_begin = nullptr, *d_task_end = nullptr,
+          *d_task_window = nullptr, *d_task_slot = nullptr, *d_red_window = nullptr,
+          *d_red_slot_off = nullptr;
+  float* d_partial = nullptr;
+  size_t partial_cap = 0;  // floats
+
+  void free_schedule() {
+    dev_free(d_group_off);
+    dev_free(d_task_begin);
+    dev_free(d_task_end);
+    dev_free(d_task_window);
+    dev_free(d_task_slot);
+    dev_free(d_red_window);
+    dev_free(d_red_slot_off);
+  }
+  ~srbcrs_plan() {
+    int cur = 0;
+    bool switched = false;
+    if (hipGetDevice(&cur) == hipSuccess && cur != device) switched = hipSetDevice(device) == hipSuccess;
+    free_schedule();
+    dev_free(d_partial);
+    dev_free(d_soff);
+    dev_free(d_sidx);
+    dev_free(d_val);
+    if (switched) (void)hipSetDevice(cur);
+  }
+};
+
+extern "C" {
+
+const char* srbcrs_last_error(void) { return g_last_error.c_str(); }
+
+const char* srbcrs_version(void) { return "mask_amd-srbcrs 0.1 gfx950"; }
+
+int srbcrs_convert_count(const int32_t* rowptr, const int32_t* colind, int32_t num_nodes,
+                         int64_t nnz, int32_t blk_h, int32_t blk_w, int32_t* soff,
+                         int64_t* total_blocks) {
+  return guarded([&] {
+    check_block_shape(blk_h, blk_w);
+    check_csr(rowptr, colind, num_nodes, nnz);
+    if (!soff || !total_blocks) fail(SRBCRS_EINVAL, "soff / total_blocks is NULL");
+    Uniq u;
+    build_uniq(rowptr, colind, num_nodes, blk_h, u);
+    *total_blocks = soff_from_uniq(u, blk_w, soff);
+  });
+}
+
+int srbcrs_convert_fill(const int32_t* rowptr, const int32_t* colind, const float* values,
+                        int32_t num_nodes, int64_t nnz, int32_t blk_h, int32_t blk_w,
+                        const int32_t* soff, int32_t* sidx, float* val, int32_t* block_partition,
+                        int32_t* edge_to_row, int32_t* edge_to_col) {
+  return guarded([&] {
+    check_block_shape(blk_h, blk_w);
+    check_csr(rowptr, colind, num_nodes, nnz);
+    if (!soff || !sidx || !val) fail(SRBCRS_EINVAL, "soff / sidx / val is NULL");
+    if (nnz > 0 && !values) fail(SRBCRS_EINVAL, "values is NULL");
+    Uniq u;
+    build_uniq(rowptr, colind, num_nodes, blk_h, u);
+    fill_from_uniq(rowptr, colind, values, num_nodes, blk_h, blk_w, u, soff, sidx, val,
+                   block_partition, edge_to_row, edge_to_col);
+  });
+}
+
+int srbcrs_plan_create(const int32_t* rowptr, const int32_t* colind, const float* values,
+                       int32_t num_nodes, int64_t nnz, int32_t blk_h, int32_t blk_w,
+                       int32_t is_device, void* stream, srbcrs_plan** out) {
+  return guarded([&] {
+    if (!out) fail(SRBCRS_EINVAL, "out is NULL");
+    *out = nullptr;
+    check_block_shape(blk_h, blk_w);
+    if (num_nodes < 1) fail(SRBCRS_EINVAL, "num_nodes must be positive");
+    if (nnz < 0 || nnz > INT32_MAX) fail(SRBCRS_EINVAL, "nnz out of range");
+    std::vector<int32_t> h_rowptr, h_colind;
+    std::vector<float> h_values;
+    const int32_t *rp = rowptr, *ci = colind;
+    const float* vv = values;
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (is_device) {
+      // the reference copies the device CSR to the host for conversion
+      // (SRBCRSSpMM_kernel.cu:203-205)
+      h_rowptr.resize((size_t)num_nodes + 1);
+      h_colind.resize((size_t)nnz);
+      h_values.resize((size_t)nnz);
+      hip_check(hipMemcpyAsync(h_rowptr.data(), rowptr, h_rowptr.size() * 4, hipMemcpyDeviceToHost, st), "copy rowptr");
+      if (nnz) {
+        hip_check(hipMemcpyAsync(h_colind.data(), colind, (size_t)nnz * 4, hipMemcpyDeviceToHost, st), "copy colind");
+        hip_check(hipMemcpyAsync(h_values.data(), values, (size_t)nnz * 4, hipMemcpyDeviceToHost, st), "copy values");
+      }
+      hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
+      rp = h_rowptr.data();
+      ci = h_colind.data();
+      vv = h_values.data();
+    }
+    check_csr(rp, ci, num_nodes, nnz);
+    if (nnz > 0 && !vv) fail(SRBCRS_EINVAL, "values is NULL");
+    auto plan = std::make_unique<srbcrs_plan>();
+    hip_check(hipGetDevice(&plan->device), "hipGetDevice");
+    plan->num_nodes = num_nodes;
+    plan->blk_h = blk_h;
+    plan->blk_w = blk_w;
+    plan->Mo = (num_nodes + blk_h - 1) / blk_h;
+    plan->nnz = nnz;
+    Uniq u;
+    build_uniq(rp, ci, num_nodes, blk_h, u);
+    plan->max_col = u.max_col;
+    plan->h_soff.resize((size_t)plan->Mo + 1);
+    plan->total = soff_from_uniq(u, blk_w, plan->h_soff.data());
+    std::vector<int32_t> sidx((size_t)(plan->total * blk_w));
+    std::vector<float> val((size_t)(plan->total * blk_h * blk_w));
+    plan->h_block_partition.assign((size_t)plan->Mo, 0);
+    plan->h_edge_to_row.assign((size_t)nnz, 0);
+    plan->h_edge_to_col.assign((size_t)nnz, 0);
+    fill_from_uniq(rp, ci, vv, num_nodes, blk_h, blk_w, u, plan->h_soff.data(), sidx.data(),
+                   val.data(), plan->h_block_partition.data(), plan->h_edge_to_row.data(),
+                   plan->h_edge_to_col.data());
+    plan->d_soff = upload(plan->h_soff);
+    plan->d_sidx = upload(sidx);
+    plan->d_val = upload(val);
+    plan->sched.policy = "row";
+    *out = plan.release();
+  });
+}
+
+void srbcrs_plan_destroy(srbcrs_plan* plan) { delete plan; }
+
+int srbcrs_plan_get(const srbcrs_plan* plan, srbcrs_plan_desc* out) {
+  return guarded([&] {
+    if (!plan || !out) fail(SRBCRS_EINVAL, "plan / out is NULL");
+    out->num_nodes = plan->num_nodes;
+    out->blk_h = plan->blk_h;
+    out->blk_w = plan->blk_w;
+    out->row_windows = plan->Mo;
+    out->max_col = plan->max_col;
+    out->device = plan->device;
+    out->nnz = plan->nnz;
+    out->total_blocks = plan->total;
+    out->d_soff = plan->d_soff;
+    out->d_sidx = plan->d_sidx;
+    out->d_val = plan->d_val;
+  });
+}
+
+int srbcrs_plan_write_edges(const srbcrs_plan* plan, int32_t* d_block_partition,
+                            int64_t block_partition_len, int32_t* d_edge_to_col,
+                            int64_t edge_to_col_len, int32_t* d_edge_to_row,
+                            int64_t edge_to_row_len, void* stream) {
+  return guarded([&] {
+    if (!plan) fail(SRBCRS_EINVAL, "plan is NULL");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    if (d_block_partition && block_partition_len >= plan->Mo && plan->Mo > 0)
+      hip_check(hipMemcpyAsync(d_block_partition, plan->h_block_partition.data(), (size_t)plan->Mo * 4,
+                               hipMemcpyHostToDevice, st), "copy block_partition");
+    if (d_edge_to_col && edge_to_col_len >= plan->nnz && plan->nnz > 0)
+      hip_check(hipMemcpyAsync(d_edge_to_col, plan->h_edge_to_col.data(), (size_t)plan->nnz * 4,
+                               hipMemcpyHostToDevice, st), "copy edge_to_col");
+    if (d_edge_to_row && edge_to_row_len >= plan->nnz && plan->nnz > 0)
+      hip_check(hipMemcpyAsync(d_edge_to_row, plan->h_edge_to_row.data(), (size_t)plan->nnz * 4,
+                               hipMemcpyHostToDevice, st), "copy edge_to_row");
+    hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
+  });
+}
+
+int srbcrs_plan_export_index(const srbcrs_plan* plan, int32_t* d_row_window_offset,
+                             int64_t row_window_offset_len, int32_t* d_tcblocktile_id,
+                             int64_t tcblocktile_id_len, void* stream) {
+  return guarded([&] {
+    if (!plan) fail(SRBCRS_EINVAL, "plan is NULL");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    const int64_t ns = (int64_t)plan->Mo + 1, nx = plan->total * plan->blk_w;
+    if (d_row_window_offset) {
+      if (row_window_offset_len < ns) fail(SRBCRS_EINVAL, "row_window_offset buffer too short (%lld < %lld)", (long long)row_window_offset_len, (long long)ns);
+      hip_check(hipMemcpyAsync(d_row_window_offset, plan->d_soff, (size_t)ns * 4, hipMemcpyDeviceToDevice, st), "copy soff");
+    }
+    if (d_tcblocktile_id && nx > 0) {
+      if (tcblocktile_id_len < nx) fail(SRBCRS_EINVAL, "tcblocktile_id buffer too short (%lld < %lld)", (long long)tcblocktile_id_len, (long long)nx);
+      hip_check(hipMemcpyAsync(d_tcblocktile_id, plan->d_sidx, (size_t)nx * 4, hipMemcpyDeviceToDevice, st), "copy sidx");
+    }
+  });
+}
+
+int srbcrs_schedule_build(const int32_t* soff, int32_t row_windows, const char* policy,
+                          int32_t param, srbcrs_schedule** out) {
+  return guarded([&] {
+    if (!out) fail(SRBCRS_EINVAL, "out is NULL");
+    *out = nullptr;
+    Schedule* s = build_schedule(soff, row_windows, policy, param);
+    auto* h = new srbcrs_schedule{std::move(*s)};
+    delete s;
+    *out = h;
+  });
+}
+
+int srbcrs_schedule_info(const srbcrs_schedule* s, int32_t* n_groups, int32_t* n_tasks,
+                         int32_t* n_slots, int32_t* n_red) {
+  return guarded([&] {
+    if (!s) fail(SRBCRS_EINVAL, "schedule is NULL");
+    if (n_groups) *n_groups = (int32_t)s->s.group_off.size() - 1;
+    if (n_tasks) *n_tasks = (int32_t)s->s.task_begin.size();
+    if (n_slots) *n_slots = s->s.n_slots;
+    if (n_red) *n_red = (int32_t)s->s.red_window.size();
+  });
+}
+
+int srbcrs_schedule_export(const srbcrs_schedule* s, int32_t* group_off, int32_t* task_begin,
+                           int32_t* task_end, int32_t* task_window, int32_t* task_slot,
+                           int32_t* red_window, int32_t* red_slot_off) {
+  return guarded([&] {
+    if (!s) fail(SRBCRS_EINVAL, "schedule is NULL");
+    auto cp = [](const std::vector<int32_t>& v, int32_t* dst) {
+      if (dst && !v.empty()) std::memcpy(dst, v.data(), v.size() * 4);
+    };
+    cp(s->s.group_off, group_off);
+    cp(s->s.task_begin, task_begin);
+    cp(s->s.task_end, task_end);
+    cp(s->s.task_window, task_window);
+    cp(s->s.task_slot, task_slot);
+    cp(s->s.red_window, red_window);
+    cp(s->s.red_slot_off, red_slot_off);
+  });
+}
+
+void srbcrs_schedule_destroy(srbcrs_schedule* s) { delete s; }
+
+int srbcrs_plan_set_schedule(srbcrs_plan* plan, const char* policy, int32_t param) {
+  return guarded([&] {
+    if (!plan) fail(SRBCRS_EINVAL, "plan is NULL");
+    int cur = 0;
+    hip_check(hipGetDevice(&cur), "hipGetDevice");
+    if (cur != plan->device) fail(SRBCRS_ESTATE, "plan lives on device %d, current device is %d", plan->device, cur);
+    Schedule* s = build_schedule(plan->h_soff.data(), plan->Mo, policy, param);
+    std::unique_ptr<Schedule> hold(s);
+    plan->free_schedule();
+    plan->sched = std::move(*s);
+    if (plan->sched.policy != "row") {
+      plan->d_group_off = upload(plan->sched.group_off);
+      plan->d_task_begin = upload(plan->sched.task_begin);
+      plan->d_task_end = upload(plan->sched.task_end);
+      plan->d_task_window = upload(plan->sched.task_window);
+      plan->d_task_slot = upload(plan->sched.task_slot);
+      plan->d_red_window = upload(plan->sched.red_window);
+      plan->d_red_slot_off = upload(plan->sched.red_slot_off);
+    }
+  });
+}
+
+int srbcrs_run(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int64_t ldb, float* d_C,
+               int64_t ldc, int64_t c_rows, void* stream) {
+  return guarded([&] {
+    if (!plan) fail(SRBCRS_EINVAL, "plan is NULL");
+    if (plan->blk_h != 16 || plan->blk_w != 8)
+      fail(SRBCRS_EINVAL, "srbcrs_run supports 16x8 plans (got %dx%d)", plan->blk_h, plan->blk_w);
+    int cur = 0;
+    hip_check(hipGetDevice(&cur), "hipGetDevice");
+    if (cur != plan->device) fail(SRBCRS_ESTATE, "plan lives on device %d, current device is %d", plan->device, cur);
+    if (N < 0 || N > INT32_MAX) fail(SRBCRS_EINVAL, "N out of range");
+    if (N == 0) return;
+    if (N % 16 != 0)
+      fail(SRBCRS_EINVAL, "SR-BCRS requires dense feature dim divisible by 16/32/64, got %lld. Please pad feature dim before run.", (long long)N);
+    if (!d_B || !d_C) fail(SRBCRS_EINVAL, "B / C is NULL");
+    if (K <= plan->max_col)
+      fail(SRBCRS_EINVAL, "dense has %lld rows but the matrix references column %d", (long long)K, plan->max_col);
+    if (ldb < N || ldc < N) fail(SRBCRS_EINVAL, "ldb / ldc must be >= N");
+    if (c_rows < plan->num_nodes) fail(SRBCRS_EINVAL, "C has %lld rows, need %d", (long long)c_rows, plan->num_nodes);
+    if ((reinterpret_cast<uintptr_t>(d_B) | reinterpret_cast<uintptr_t>(d_C)) % 4)
+      fail(SRBCRS_EINVAL, "B / C must be 4-byte aligned");
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    // vector width: the widest of 4/2/1 that N, ldb, ldc and the pointers allow
+    int vec = 4;
+    while (vec > 1 && ((N % (16 * vec)) || (ldb % vec) || (ldc % vec) ||
+                       (reinterpret_cast<uintptr_t>(d_B) % (4 * vec)) ||
+                       (reinterpret_cast<uintptr_t>(d_C) % (4 * vec))))
+      vec /= 2;
+    if (plan->sched.policy == "row") {
+      srbcrs::RowArgs a{d_B, d_C, plan->d_soff, plan->d_sidx, plan->d_val,
+                        plan->num_nodes, (int)N, plan->Mo, ldb, ldc};
+      hip_check(srbcrs::launch_row(a, vec, st), "launch spmm16x8_row");
+      return;
+    }
+    const Schedule& s = plan->sched;
+    const size_t need = (size_t)s.n_slots * 16 * (size_t)ldc;
+    if (need > plan->partial_cap) {
+      hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
+      dev_free(plan->d_partial);
+      plan->partial_cap = 0;
+      plan->d_partial = dev_alloc<float>(need);
+      plan->partial_cap = need;
+    }
+    srbcrs::TaskArgs ta{d_B, d_C, plan->d_partial, plan->d_sidx, plan->d_val,
+                        plan->d_group_off, plan->d_task_begin, plan->d_task_end,
+                        plan->d_task_window, plan->d_task_slot,
+                        (int)s.group_off.size() - 1, plan->num_nodes, (int)N, ldb, ldc};
+    hip_check(srbcrs::launch_tasks(ta, vec, st), "launch spmm16x8_tasks");
+    srbcrs::ReduceArgs ra{plan->d_partial, d_C, plan->d_red_window, plan->d_red_slot_off,
+                          (int)s.red_window.size(), plan->num_nodes, (int)N, ldc};
+    hip_check(srbcrs::launch_reduce(ra, vec, st), "launch segment_reduce");
+  });
+}
+
+int srbcrs_csr_spmm(const int32_t* d_rowptr, const int32_t* d_colind, const float* d_values,
+                    int32_t M, int64_t nnz, int32_t max_col, const float* d_B, int64_t K, int64_t N,
+                    int64_t ldb, float* d_C, int64_t ldc, void* stream) {
+  return guarded([&] {
+    if (M < 0) fail(SRBCRS_EINVAL, "M must be >= 0");
+    if (N < 0 || N > INT32_MAX) fail(SRBCRS_EINVAL, "N out of range");
+    if (M == 0 || N == 0) return;
+    if (!d_rowptr || !d_B || !d_C) fail(SRBCRS_EINVAL, "NULL pointer");
+    if (nnz > 0 && (!d_colind || !d_values)) fail(SRBCRS_EINVAL, "NULL colind / values");
+    if (nnz > 0 && (max_col < 0 || max_col >= K))
+      fail(SRBCRS_EINVAL, "max_col %d out of range for dense with %lld rows", max_col, (long long)K);
+    if (ldb < N || ldc < N) fail(SRBCRS_EINVAL, "ldb / ldc must be >= N");
+    int vec = 4;
+    while (vec > 1 && ((N % (64 * vec)) || (ldb % vec) || (ldc % vec) ||
+                       (reinterpret_cast<uintptr_t>(d_B) % (4 * vec)) ||
+                       (reinterpret_cast<uintptr_t>(d_C) % (4 * vec))))
+      vec /= 2;
+    srbcrs::CsrArgs a{d_rowptr, d_colind, d_values, d_B, d_C, M, (int)N, ldb, ldc};
+    hip_check(srbcrs::launch_csr(a, vec, static_cast<hipStream_t>(stream)), "launch csr_spmm_rowwave");
+  });
+}
+
+}  // extern "C"

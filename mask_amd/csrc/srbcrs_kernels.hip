@@ -1,0 +1,405 @@
+// SR-BCRS 16x8 fp32 SpMM kernels for gfx950 (CDNA4, wave64).
+//
+// C[M x N] = A[M x K] * B[K x N], A in SR-BCRS 16x8:
+//   soff[Mo+1]   block offsets per 16-row window
+//   sidx[8*nb]   the 8 B-row (column) indices of each block
+//   val[128*nb]  the block values, 16x8 row-major with CuTe Swizzle<2,2,3>
+//                applied to the offset: pos(r,c) = o ^ ((o & 0x60) >> 3),
+//                o = 8r + c.
+// This is the data the reference's sr_bcrs_spmm_kernel_tf32<16,64,8>
+// consumes (examples/src_fp32/sr_bcrs/testbed/kernel.inc:1590-1700); the
+// arithmetic here is native fp32 MFMA instead of TF32 MMA.
+//
+// MFMA mapping.  v_mfma_f32_16x16x4_f32 (wave64) computes D(16x16) +=
+// A(16x4) * B(4x16) with lane l holding A[l%16][l/16], B[l/16][l%16] and
+// D[4*(l/16)+r][l%16], r = 0..3.  One 16x8 block is two such k-steps; the
+// 8 block columns are split as k-step 0 = {0,2,4,6}, k-step 1 = {1,3,5,7},
+// so lane (i = l%16, k = l/16) needs A[i][2k] and A[i][2k+1].  The swizzle
+// only touches offset bits 2..3, so those two values sit next to each other
+// in memory: one 8-byte load per lane fetches the lane's A fragment.
+//
+// Column mapping.  A wave owns 16*VEC*G output columns.  In column group g
+// lane j = l%16 owns columns base + 16*VEC*g + VEC*j + s (s < VEC): one
+// VEC-wide vector load per (B row, g) per lane, VEC MFMAs per k-step and g.
+// For VEC = 4 a wave's B load covers four 256-byte row segments.
+//
+// No LDS: every B element is used by exactly one wave (waves of a workgroup
+// split N), so staging through LDS adds no reuse; latency is hidden by a
+// register ring DEPTH blocks deep (indices one more ring ahead).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "srbcrs_kernels.h"
+
+namespace srbcrs {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+
+template <int VEC> struct VecT;
+template <> struct VecT<1> { typedef float type; };
+template <> struct VecT<2> { typedef f2 type; };
+template <> struct VecT<4> { typedef f4 type; };
+
+template <int VEC>
+__device__ __forceinline__ float vget(const typename VecT<VEC>::type& v, int s);
+template <> __device__ __forceinline__ float vget<1>(const float& v, int) { return v; }
+template <> __device__ __forceinline__ float vget<2>(const f2& v, int s) { return v[s]; }
+template <> __device__ __forceinline__ float vget<4>(const f4& v, int s) { return v[s]; }
+
+__device__ __forceinline__ int swz16x8(int o) { return o ^ ((o & 0x60) >> 3); }
+
+// Map the hardware workgroup id to a logical one so that each XCD (the
+// dispatcher deals workgroups round-robin over the 8 XCDs) receives a
+// contiguous range of logical ids: neighbouring row windows, which share B
+// rows in banded matrices, then share one L2.
+__device__ __forceinline__ int64_t xcd_remap(int64_t id, int64_t n) {
+  const int64_t q = n / kNumXcd, r = n % kNumXcd;
+  const int64_t x = id % kNumXcd, t = id / kNumXcd;
+  return x * q + (x < r ? x : r) + t;
+}
+
+template <int VEC, int G>
+struct Frag {
+  typedef typename VecT<VEC>::type V;
+  f2 a;          // A[i][2k], A[i][2k+1]
+  V b0[G];       // B[sidx[2k]][cols of g]
+  V b1[G];       // B[sidx[2k+1]][cols of g]
+};
+
+template <int VEC, int G>
+__device__ __forceinline__ void load_frag(Frag<VEC, G>& f, const float* __restrict__ B,
+                                          const float* __restrict__ val, int64_t blk, int2 rows,
+                                          int a_off, int64_t ldb, int col0) {
+  typedef typename VecT<VEC>::type V;
+  f.a = *reinterpret_cast<const f2*>(val + blk * 128 + a_off);
+  const float* r0 = B + (int64_t)rows.x * ldb + col0;
+  const float* r1 = B + (int64_t)rows.y * ldb + col0;
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    f.b0[g] = *reinterpret_cast<const V*>(r0 + 16 * VEC * g);
+    f.b1[g] = *reinterpret_cast<const V*>(r1 + 16 * VEC * g);
+  }
+}
+
+template <int VEC, int G>
+__device__ __forceinline__ void mma_frag(const Frag<VEC, G>& f, f4 (&acc)[G][VEC]) {
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int s = 0; s < VEC; ++s) {
+      acc[g][s] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a.x, vget<VEC>(f.b0[g], s), acc[g][s], 0, 0, 0);
+      acc[g][s] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a.y, vget<VEC>(f.b1[g], s), acc[g][s], 0, 0, 0);
+    }
+  }
+}
+
+// Accumulate blocks [b0, b1) of one window into acc with a DEPTH-deep ring.
+template <int VEC, int G, int DEPTH>
+__device__ __forceinline__ void accumulate_blocks(f4 (&acc)[G][VEC], const float* __restrict__ B,
+                                                  const int* __restrict__ sidx,
+                                                  const float* __restrict__ val, int64_t b0,
+                                                  int64_t b1, int64_t ldb, int col0, int lane) {
+  const int k = lane >> 4;
+  const int i = lane & 15;
+  const int a_off = swz16x8(8 * i + 2 * k);
+  Frag<VEC, G> f[DEPTH];
+  int2 idx[DEPTH];
+  const int64_t last = b1 - 1;
+  // prologue: indices for blocks b0 .. b0+2*DEPTH-1, data for b0 .. b0+DEPTH-1
+#pragma unroll
+  for (int d = 0; d < DEPTH; ++d) {
+    int64_t blk = b0 + d < last ? b0 + d : last;
+    int2 rows = *reinterpret_cast<const int2*>(sidx + blk * 8 + 2 * k);
+    load_frag<VEC, G>(f[d], B, val, blk, rows, a_off, ldb, col0);
+    int64_t nblk = b0 + DEPTH + d < last ? b0 + DEPTH + d : last;
+    idx[d] = *reinterpret_cast<const int2*>(sidx + nblk * 8 + 2 * k);
+  }
+  for (int64_t base = b0; base < b1; base += DEPTH) {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      const int64_t blk = base + d;
+      if (blk < b1) mma_frag<VEC, G>(f[d], acc);
+      const int64_t nblk = blk + DEPTH;
+      if (nblk < b1) {
+        load_frag<VEC, G>(f[d], B, val, nblk, idx[d], a_off, ldb, col0);
+        const int64_t nn = nblk + DEPTH < last ? nblk + DEPTH : last;
+        idx[d] = *reinterpret_cast<const int2*>(sidx + nn * 8 + 2 * k);
+      }
+    }
+  }
+}
+
+// Store a 16 x (16*VEC*G) accumulator tile.  row0 is the tile's first row in
+// `out`, rows >= row_limit are skipped (M % 16 != 0).
+template <int VEC, int G>
+__device__ __forceinline__ void store_tile(const f4 (&acc)[G][VEC], float* __restrict__ out,
+                                           int64_t row0, int64_t row_limit, int64_t ldc, int col0,
+                                           int lane) {
+  typedef typename VecT<VEC>::type V;
+  const int k = lane >> 4;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int64_t row = row0 + 4 * k + r;
+    if (row < row_limit) {
+      float* p = out + row * ldc + col0;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        V v;
+        if constexpr (VEC == 1) {
+          v = acc[g][0][r];
+        } else {
+#pragma unroll
+          for (int s = 0; s < VEC; ++s) v[s] = acc[g][s][r];
+        }
+        __builtin_nontemporal_store(v, reinterpret_cast<V*>(p + 16 * VEC * g));
+      }
+    }
+  }
+}
+
+// One workgroup = WAVES waves on one (row window, column chunk); a column
+// chunk is WAVES * 16*VEC*G columns.  Grid is 1-D over Mo * n_chunks.
+template <int VEC, int G, int WAVES, int DEPTH>
+__global__ __launch_bounds__(64 * WAVES) void spmm16x8_row(
+    const float* __restrict__ B, float* __restrict__ C, const int* __restrict__ soff,
+    const int* __restrict__ sidx, const float* __restrict__ val, int M, int N, int64_t ldb,
+    int64_t ldc, int n_chunks) {
+  constexpr int WCOLS = 16 * VEC * G;
+  const int64_t nwg = (int64_t)gridDim.x;
+  const int64_t lid = xcd_remap(blockIdx.x, nwg);
+  const int w = (int)(lid / n_chunks);
+  const int chunk = (int)(lid % n_chunks);
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wcol = (chunk * WAVES + wave) * WCOLS;
+  if (wcol >= N) return;
+  const int col0 = wcol + VEC * (lane & 15);
+  f4 acc[G][VEC];
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int s = 0; s < VEC; ++s) acc[g][s] = f4{0.f, 0.f, 0.f, 0.f};
+  const int64_t b0 = soff[w], b1 = soff[w + 1];
+  if (b0 < b1) accumulate_blocks<VEC, G, DEPTH>(acc, B, sidx, val, b0, b1, ldb, col0, lane);
+  store_tile<VEC, G>(acc, C, (int64_t)w * 16, M, ldc, col0, lane);
+}
+
+// Task-mapped variant: workgroup group g runs tasks [group_off[g],
+// group_off[g+1]); task t accumulates blocks [task_begin[t], task_end[t]) of
+// window task_window[t] and writes the 16-row tile either straight into C
+// (task_slot[t] < 0) or into partial slot task_slot[t] (16 x N, row stride
+// ldc) for the segment-reduce kernel.  No atomics: every output element has
+// exactly one writer per launch.
+template <int VEC, int G, int WAVES, int DEPTH>
+__global__ __launch_bounds__(64 * WAVES) void spmm16x8_tasks(
+    const float* __restrict__ B, float* __restrict__ C, float* __restrict__ partial,
+    const int* __restrict__ sidx, const float* __restrict__ val,
+    const int* __restrict__ group_off, const int* __restrict__ task_begin,
+    const int* __restrict__ task_end, const int* __restrict__ task_window,
+    const int* __restrict__ task_slot, int M, int N, int64_t ldb, int64_t ldc, int n_chunks) {
+  constexpr int WCOLS = 16 * VEC * G;
+  const int64_t nwg = (int64_t)gridDim.x;
+  const int64_t lid = xcd_remap(blockIdx.x, nwg);
+  const int grp = (int)(lid / n_chunks);
+  const int chunk = (int)(lid % n_chunks);
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wcol = (chunk * WAVES + wave) * WCOLS;
+  if (wcol >= N) return;
+  const int col0 = wcol + VEC * (lane & 15);
+  const int t0 = group_off[grp], t1 = group_off[grp + 1];
+  for (int t = t0; t < t1; ++t) {
+    f4 acc[G][VEC];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int s = 0; s < VEC; ++s) acc[g][s] = f4{0.f, 0.f, 0.f, 0.f};
+    const int64_t b0 = task_begin[t], b1 = task_end[t];
+    if (b0 < b1) accumulate_blocks<VEC, G, DEPTH>(acc, B, sidx, val, b0, b1, ldb, col0, lane);
+    const int slot = task_slot[t];
+    if (slot < 0) {
+      store_tile<VEC, G>(acc, C, (int64_t)task_window[t] * 16, M, ldc, col0, lane);
+    } else {
+      store_tile<VEC, G>(acc, partial, (int64_t)slot * 16, (int64_t)(slot + 1) * 16, ldc, col0, lane);
+    }
+  }
+}
+
+// out rows of window red_window[i] = sum over slots [red_slot_off[i],
+// red_slot_off[i+1]) of the partial tiles, in slot order (deterministic;
+// zero slots give zeros).  The atomic-free counterpart of the reference's
+// reduce_tcf_segments (examples/src_fp32/acc/testbed/custom_format_e2e.cu:
+// 832-853).  One thread per VEC consecutive columns.
+template <int VEC>
+__global__ __launch_bounds__(256) void segment_reduce(const float* __restrict__ partial,
+                                                      float* __restrict__ C,
+                                                      const int* __restrict__ red_window,
+                                                      const int* __restrict__ red_slot_off,
+                                                      int n_red, int M, int N, int64_t ldc) {
+  typedef typename VecT<VEC>::type V;
+  const int64_t nv = N / VEC;
+  const int64_t per = 16 * nv;
+  const int64_t total = (int64_t)n_red * per;
+  for (int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; id < total;
+       id += (int64_t)gridDim.x * blockDim.x) {
+    const int i = (int)(id / per);
+    const int64_t within = id % per;
+    const int r = (int)(within / nv);
+    const int64_t cv = within % nv;
+    const int64_t row = (int64_t)red_window[i] * 16 + r;
+    if (row >= M) continue;
+    V s;
+    if constexpr (VEC == 1) s = 0.f; else { for (int q = 0; q < VEC; ++q) s[q] = 0.f; }
+    for (int sl = red_slot_off[i]; sl < red_slot_off[i + 1]; ++sl)
+      s += *reinterpret_cast<const V*>(partial + ((int64_t)sl * 16 + r) * ldc + VEC * cv);
+    *reinterpret_cast<V*>(C + row * ldc + VEC * cv) = s;
+  }
+}
+
+// CSR SpMM, one wave per row: lane owns VEC*NV consecutive columns per
+// 64*VEC-column pass.  Edge-ordered fp32 accumulation, the arithmetic of the
+// reference's csr_spmm_value_kernel (examples/src_fp32/sr_bcrs/testbed/
+// SRBCRSSpMM_kernel.cu:66-87), laid out for wave64 vector loads.
+template <int VEC, int UNROLL>
+__global__ __launch_bounds__(256) void csr_spmm_rowwave(
+    const int* __restrict__ rowptr, const int* __restrict__ colind,
+    const float* __restrict__ values, const float* __restrict__ B, float* __restrict__ C, int M,
+    int N, int64_t ldb, int64_t ldc) {
+  typedef typename VecT<VEC>::type V;
+  const int64_t nwg = (int64_t)gridDim.x;
+  const int64_t lid = xcd_remap(blockIdx.x, nwg);
+  const int64_t row = lid * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (row >= M) return;
+  const int e0 = rowptr[row], e1 = rowptr[row + 1];
+  for (int c = VEC * lane; c < N; c += 64 * VEC) {
+    V acc;
+    if constexpr (VEC == 1) acc = 0.f; else { for (int s = 0; s < VEC; ++s) acc[s] = 0.f; }
+    int e = e0;
+    for (; e + UNROLL <= e1; e += UNROLL) {
+      V bv[UNROLL];
+      float av[UNROLL];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        const int col = colind[e + u];
+        av[u] = values[e + u];
+        bv[u] = *reinterpret_cast<const V*>(B + (int64_t)col * ldb + c);
+      }
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) acc += av[u] * bv[u];
+    }
+    for (; e < e1; ++e) {
+      const int col = colind[e];
+      acc += values[e] * *reinterpret_cast<const V*>(B + (int64_t)col * ldb + c);
+    }
+    *reinterpret_cast<V*>(C + row * ldc + c) = acc;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host launchers.
+
+static int pick_waves(int N, int wcols) {
+  int w = (N + wcols - 1) / wcols;
+  return w >= 4 ? 4 : (w >= 2 ? 2 : 1);
+}
+
+template <int VEC, int G, int DEPTH>
+static hipError_t launch_row_vg(const RowArgs& a, hipStream_t st) {
+  constexpr int WCOLS = 16 * VEC * G;
+  const int waves = pick_waves(a.N, WCOLS);
+  const int chunk_cols = waves * WCOLS;
+  const int n_chunks = (a.N + chunk_cols - 1) / chunk_cols;
+  const int64_t nwg = (int64_t)a.Mo * n_chunks;
+  if (nwg == 0) return hipSuccess;
+  dim3 grid((unsigned)nwg);
+  switch (waves) {
+    case 4:
+      hipLaunchKernelGGL((spmm16x8_row<VEC, G, 4, DEPTH>), grid, dim3(256), 0, st, a.B, a.C, a.soff,
+                         a.sidx, a.val, a.M, a.N, a.ldb, a.ldc, n_chunks);
+      break;
+    case 2:
+      hipLaunchKernelGGL((spmm16x8_row<VEC, G, 2, DEPTH>), grid, dim3(128), 0, st, a.B, a.C, a.soff,
+                         a.sidx, a.val, a.M, a.N, a.ldb, a.ldc, n_chunks);
+      break;
+    default:
+      hipLaunchKernelGGL((spmm16x8_row<VEC, G, 1, DEPTH>), grid, dim3(64), 0, st, a.B, a.C, a.soff,
+                         a.sidx, a.val, a.M, a.N, a.ldb, a.ldc, n_chunks);
+      break;
+  }
+  return hipGetLastError();
+}
+
+template <int VEC, int G, int DEPTH>
+static hipError_t launch_tasks_vg(const TaskArgs& a, hipStream_t st) {
+  constexpr int WCOLS = 16 * VEC * G;
+  const int waves = pick_waves(a.N, WCOLS);
+  const int chunk_cols = waves * WCOLS;
+  const int n_chunks = (a.N + chunk_cols - 1) / chunk_cols;
+  const int64_t nwg = (int64_t)a.n_groups * n_chunks;
+  if (nwg == 0) return hipSuccess;
+  dim3 grid((unsigned)nwg);
+#define SRBCRS_LAUNCH_TASKS(W)                                                                   \
+  hipLaunchKernelGGL((spmm16x8_tasks<VEC, G, W, DEPTH>), grid, dim3(64 * W), 0, st, a.B, a.C,   \
+                     a.partial, a.sidx, a.val, a.group_off, a.task_begin, a.task_end,            \
+                     a.task_window, a.task_slot, a.M, a.N, a.ldb, a.ldc, n_chunks)
+  switch (waves) {
+    case 4: SRBCRS_LAUNCH_TASKS(4); break;
+    case 2: SRBCRS_LAUNCH_TASKS(2); break;
+    default: SRBCRS_LAUNCH_TASKS(1); break;
+  }
+#undef SRBCRS_LAUNCH_TASKS
+  return hipGetLastError();
+}
+
+// vec (4, 2 or 1; 16*vec divides N) is chosen by the caller from N, the
+// leading dimensions and pointer alignment; G = 2 column groups per wave when
+// the 128-column wave tile divides N.
+hipError_t launch_row(const RowArgs& a, int vec, hipStream_t st) {
+  if (vec == 4) return a.N % 128 == 0 ? launch_row_vg<4, 2, kDepth>(a, st) : launch_row_vg<4, 1, kDepth>(a, st);
+  if (vec == 2) return launch_row_vg<2, 1, kDepth>(a, st);
+  return launch_row_vg<1, 1, kDepth>(a, st);
+}
+
+hipError_t launch_tasks(const TaskArgs& a, int vec, hipStream_t st) {
+  if (vec == 4) return a.N % 128 == 0 ? launch_tasks_vg<4, 2, kDepth>(a, st) : launch_tasks_vg<4, 1, kDepth>(a, st);
+  if (vec == 2) return launch_tasks_vg<2, 1, kDepth>(a, st);
+  return launch_tasks_vg<1, 1, kDepth>(a, st);
+}
+
+hipError_t launch_reduce(const ReduceArgs& a, int vec, hipStream_t st) {
+  if (a.n_red == 0) return hipSuccess;
+  const int64_t total = (int64_t)a.n_red * 16 * (a.N / vec);
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  if (vec == 4)
+    hipLaunchKernelGGL(segment_reduce<4>, dim3((unsigned)blocks), dim3(256), 0, st, a.partial, a.C,
+                       a.red_window, a.red_slot_off, a.n_red, a.M, a.N, a.ldc);
+  else if (vec == 2)
+    hipLaunchKernelGGL(segment_reduce<2>, dim3((unsigned)blocks), dim3(256), 0, st, a.partial, a.C,
+                       a.red_window, a.red_slot_off, a.n_red, a.M, a.N, a.ldc);
+  else
+    hipLaunchKernelGGL(segment_reduce<1>, dim3((unsigned)blocks), dim3(256), 0, st, a.partial, a.C,
+                       a.red_window, a.red_slot_off, a.n_red, a.M, a.N, a.ldc);
+  return hipGetLastError();
+}
+
+// vec: columns per lane per pass (64*vec divides N, or 1).
+hipError_t launch_csr(const CsrArgs& a, int vec, hipStream_t st) {
+  const int64_t nwg = ((int64_t)a.M + 3) / 4;
+  if (nwg == 0) return hipSuccess;
+  dim3 grid((unsigned)nwg);
+  if (vec == 4)
+    hipLaunchKernelGGL((csr_spmm_rowwave<4, 4>), grid, dim3(256), 0, st, a.rowptr, a.colind,
+                       a.values, a.B, a.C, a.M, a.N, a.ldb, a.ldc);
+  else if (vec == 2)
+    hipLaunchKernelGGL((csr_spmm_rowwave<2, 4>), grid, dim3(256), 0, st, a.rowptr, a.colind,
+                       a.values, a.B, a.C, a.M, a.N, a.ldb, a.ldc);
+  else
+    hipLaunchKernelGGL((csr_spmm_rowwave<1, 4>), grid, dim3(256), 0, st, a.rowptr, a.colind,
+                       a.values, a.B, a.C, a.M, a.N, a.ldb, a.ldc);
+  return hipGetLastError();
+}
+
+}  // namespace srbcrs
