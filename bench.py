@@ -39,7 +39,22 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline leg")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-check", action="store_true")
+    ap.add_argument("--copy-calibration-mb", type=int, default=0,
+                    help="only run an elementwise copy of this many MiB (5 launches) to calibrate "
+                         "rocprofv3 FETCH_SIZE / WRITE_SIZE against a known byte count")
     return ap.parse_args()
+
+
+def copy_calibration(mib):
+    """Known-traffic reference kernel: out = in * 1 over mib MiB reads + writes."""
+    import torch
+    n = mib * (1 << 20) // 4
+    a = torch.ones(n, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    for _ in range(5):
+        torch.mul(a, 1.0, out=b)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_read": n * 4, "copy_calibration_bytes_written": n * 4}))
 
 
 def algorithmic_bytes(M, N, Mo, nb, nnz, kernel):
@@ -57,6 +72,10 @@ def main():
         print(json.dumps({"error": "this benchmark measures one GPU; --gpus must be 1 "
                                    "(the SpMM path is single-GPU, sharding is design-only)"}))
         sys.exit(2)
+
+    if args.copy_calibration_mb:
+        copy_calibration(args.copy_calibration_mb)
+        return
 
     import torch
     from mask_amd import datasets

@@ -1,0 +1,200 @@
+"""Host-side parity (no GPU): the C-ABI library's converter and schedules
+against the oracle, its exports against include/srbcrs.h, error paths, and
+the Python drop-in module's argument checks."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from mask_amd import _capi, datasets
+from oracle import oracle
+from tests.helpers import random_csr
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def _header_functions():
+    text = (ROOT / "include" / "srbcrs.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(srbcrs_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    names = _header_functions()
+    assert len(names) >= 15
+    assert sorted(_capi.EXPORTS) == names
+    L = _capi.lib()
+    for n in names:
+        assert hasattr(L, n), n
+    assert b"gfx950" in L.srbcrs_version()
+
+
+def _same(a, b):
+    for k in ("soff", "sidx", "block_partition", "edge_to_row", "edge_to_col"):
+        assert np.array_equal(a[k], b[k]), k
+    assert a["total"] == b["total"]
+    assert a["val"].tobytes() == b["val"].tobytes()
+
+
+@pytest.mark.parametrize("bh,bw", [(16, 8), (32, 32)])
+@pytest.mark.parametrize("case", range(6))
+def test_converter_matches_oracle(case, bh, bw):
+    M = [1, 15, 16, 17, 250, 1000][case]
+    K = [1, 40, 300, 9, 700, 5000][case]
+    rowptr, colind, values = random_csr(M, K, min(0.5, 3.0 / K + 0.02), seed=case, unsorted=case % 2 == 0,
+                                        duplicates=case >= 3, empty_rows=0.25, heavy_rows=2 if M > 100 else 0,
+                                        heavy_len=min(K, 600))
+    _same(_capi.convert_host(rowptr, colind, values, M, bh, bw), oracle.convert(rowptr, colind, values, M, bh, bw))
+
+
+@pytest.mark.parametrize("name", ["uniform-4096", "uniform-65536", "banded-524288", "rmat-2^20", "gcn-232965"])
+def test_converter_matches_oracle_on_workloads(name):
+    m = datasets.make_config(name, scale_down=1 if name == "uniform-4096" else 32)
+    _same(_capi.convert_host(m.rowptr, m.colind, m.values, m.M), oracle.convert(m.rowptr, m.colind, m.values, m.M))
+
+
+def test_converter_full_size_uniform_65536():
+    """The metric's workload at full size, bit-exact (1M nonzeros)."""
+    m = datasets.make_config("uniform-65536")
+    _same(_capi.convert_host(m.rowptr, m.colind, m.values, m.M), oracle.convert(m.rowptr, m.colind, m.values, m.M))
+
+
+def test_converter_rejects_bad_input():
+    rowptr = np.array([0, 2, 1], np.int32)
+    with pytest.raises(_capi.SrbcrsError, match="non-decreasing") as e:
+        _capi.convert_host(rowptr, np.array([0, 1], np.int32), np.ones(2, np.float32), 2)
+    assert e.value.code == _capi.SRBCRS_EINVAL
+    with pytest.raises(_capi.SrbcrsError, match="negative"):
+        _capi.convert_host(np.array([0, 1], np.int32), np.array([-3], np.int32), np.ones(1, np.float32), 1)
+    with pytest.raises(_capi.SrbcrsError, match="16x8 or 32x32"):
+        _capi.convert_host(np.array([0, 1], np.int32), np.array([0], np.int32), np.ones(1, np.float32), 1, 16, 16)
+    with pytest.raises(_capi.SrbcrsError, match="exceeds colind length"):
+        _capi.convert_host(np.array([0, 5], np.int32), np.array([0], np.int32), np.ones(1, np.float32), 1)
+    with pytest.raises(_capi.SrbcrsError, match="num_nodes"):
+        _capi.convert_host(np.array([0], np.int32), np.zeros(0, np.int32), np.zeros(0, np.float32), 0)
+
+
+# ---- schedules ------------------------------------------------------------------
+
+def _soff_cases():
+    rng = np.random.default_rng(0)
+    yield np.array([0], np.int32)
+    yield np.cumsum([0, 3, 0, 5, 2]).astype(np.int32)
+    yield np.cumsum([0, 1, 10, 1, 0]).astype(np.int32)
+    yield np.cumsum([0] + [2] * 100 + [200]).astype(np.int32)
+    for _ in range(4):
+        lens = rng.zipf(1.6, size=rng.integers(1, 400)).clip(0, 3000)
+        lens[rng.random(lens.size) < 0.2] = 0
+        yield np.cumsum(np.concatenate([[0], lens])).astype(np.int32)
+
+
+def _check_cover(s, soff):
+    """Every block is in exactly one task of its window; every window is
+    written exactly once (one direct task, or a reduce entry)."""
+    Mo = soff.size - 1
+    tb, te, tw, ts = s["task_begin"], s["task_end"], s["task_window"], s["task_slot"]
+    covered = np.zeros(int(soff[-1]), np.int32)
+    for b, e, w in zip(tb, te, tw):
+        assert soff[w] <= b <= e <= soff[w + 1]
+        covered[b:e] += 1
+    assert (covered == 1).all()
+    assert s["group_off"][0] == 0 and s["group_off"][-1] == tb.size
+    assert (np.diff(s["group_off"]) >= 0).all()
+    writes = np.zeros(Mo, np.int32)
+    for w, sl in zip(tw, ts):
+        if sl < 0:
+            writes[w] += 1
+    slots_seen = []
+    for i, w in enumerate(s["red_window"]):
+        writes[w] += 1
+        lo, hi = s["red_slot_off"][i], s["red_slot_off"][i + 1]
+        slots_seen += list(range(lo, hi))
+        # the reduce sums this window's task slots, in task order
+        assert [int(x) for x in ts[(tw == w) & (ts >= 0)]] == list(range(lo, hi))
+    assert (writes == 1).all()
+    assert sorted(slots_seen) == list(range(s["n_slots"]))
+
+
+@pytest.mark.parametrize("workload", [0, 4, 64])
+def test_strict_lb_matches_oracle(workload):
+    for soff in _soff_cases():
+        s = _capi.build_schedule(soff, "strict_lb", workload)
+        o = oracle.strict_lb(soff, workload or 64)
+        assert s["task_begin"].tolist() == o["frag_begin"][:-1].tolist()
+        assert s["task_end"].tolist() == o["frag_begin"][1:].tolist()
+        assert s["task_window"].tolist() == o["frag_window"].tolist()
+        assert s["group_off"].tolist() == o["group_off"].tolist()
+        _check_cover(s, soff)
+
+
+def test_multi_bind_matches_oracle():
+    for soff in _soff_cases():
+        s = _capi.build_schedule(soff, "multi_bind")
+        o = oracle.multi_bind(soff)
+        assert s["task_window"].tolist() == o["part_window"].tolist()
+        assert s["task_begin"].tolist() == o["part_off"][:-1].tolist()
+        assert s["task_end"].tolist() == o["part_off"][1:].tolist()
+        assert s["group_off"].tolist() == list(range(o["part_window"].size + 1))
+        _check_cover(s, soff)
+
+
+@pytest.mark.parametrize("cap", [0, 1, 3, 32])
+def test_split_matches_oracle(cap):
+    for soff in _soff_cases():
+        s = _capi.build_schedule(soff, "split", cap)
+        o = oracle.segment_auto(soff, cap)
+        assert s["task_end"].tolist() == o["seg_end"].tolist()
+        wso = o["win_seg_off"]
+        assert s["task_window"].tolist() == np.repeat(np.arange(soff.size - 1), np.diff(wso)).tolist()
+        _check_cover(s, soff)
+
+
+def test_row_schedule_and_errors():
+    soff = np.cumsum([0, 3, 0, 5]).astype(np.int32)
+    s = _capi.build_schedule(soff, "row")
+    assert s["task_begin"].tolist() == [0, 3, 3] and s["task_end"].tolist() == [3, 3, 8]
+    assert (s["task_slot"] == -1).all() and s["n_slots"] == 0 and s["red_window"].size == 0
+    with pytest.raises(_capi.SrbcrsError, match="unknown schedule policy"):
+        _capi.build_schedule(soff, "bogus")
+    with pytest.raises(_capi.SrbcrsError, match="non-decreasing"):
+        _capi.build_schedule(np.array([0, 5, 2], np.int32), "row")
+
+
+# ---- drop-in module argument checks (no GPU needed to reach them) ------------------
+
+def test_dropin_rejects_host_tensors():
+    torch = pytest.importorskip("torch")
+    from mask_amd import SRBCRSSpMM as S
+    t = torch.zeros(4, dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="colind must be a CUDA tensor"):
+        S.preprocess_gpu_16x8(t, t, t.float(), 3, 16, 8, t, t, t)
+    with pytest.raises(RuntimeError, match="dense must be a CUDA tensor"):
+        S.run_SRBCRS_16x8(t.float().reshape(2, 2), t, t, t, t, 3, 4, "")
+
+
+def test_tile_b_selection(monkeypatch):
+    from mask_amd import SRBCRSSpMM as S
+    monkeypatch.delenv("SRBCRS_TILE_B", raising=False)
+    assert S._tile_b_for(512) == 64 and S._tile_b_for(96) == 32 and S._tile_b_for(48) == 16
+    assert S._tile_b_for(40) == 0
+    monkeypatch.setenv("SRBCRS_TILE_B", "32")
+    assert S._tile_b_for(64) == 32
+    with pytest.raises(RuntimeError, match="SRBCRS_TILE_B=32 requires"):
+        S._tile_b_for(48)
+    monkeypatch.setenv("SRBCRS_TILE_B", "8")
+    with pytest.raises(RuntimeError, match="Invalid SRBCRS_TILE_B=8"):
+        S._tile_b_for(64)
+
+
+def test_exeplan_schedule_parsing(monkeypatch):
+    from mask_amd import SRBCRSSpMM as S
+    monkeypatch.delenv("SPARSENE_SRBCRS_SCHEDULE", raising=False)
+    assert S._schedule_from_exeplan("") is None
+    assert S._schedule_from_exeplan("whatever") is None
+    assert S._schedule_from_exeplan("strict_lb:32") == ("strict_lb", 32)
+    monkeypatch.setenv("SPARSENE_SRBCRS_SCHEDULE", "split")
+    assert S._schedule_from_exeplan("") == ("split", 0)
