@@ -39,6 +39,11 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline leg")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-check", action="store_true")
+    ap.add_argument("--depth", type=int, default=0, help="kernel knob: blocks in flight per wave (2/4/8)")
+    ap.add_argument("--tile-b", type=int, default=0, help="kernel knob: 16/32/64")
+    ap.add_argument("--wg-cols", type=int, default=0, help="kernel knob: columns per workgroup")
+    ap.add_argument("--grid-order", type=int, default=0, help="kernel knob: 1 chunk-major, 2 window-major")
+    ap.add_argument("--wpw", type=int, default=0, help="kernel knob: row windows streamed per wave")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="only run an elementwise copy of this many MiB (5 launches) to calibrate "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE against a known byte count")
@@ -108,7 +113,8 @@ def main():
     max_col = plan.max_col
 
     if args.kernel == "srbcrs":
-        step = lambda: plan.run(B, C)
+        step = lambda: plan.run(B, C, depth=args.depth, tile_b=args.tile_b, wg_cols=args.wg_cols,
+                                grid_order=args.grid_order, windows_per_wave=args.wpw)
     else:
         step = lambda: csr_spmm(rowptr_d, colind_d, values_d, B, m.M, max_col=max_col, out=C)
 
@@ -155,7 +161,9 @@ def main():
         "config": {"workload": m.name, "M": m.M, "K": m.K, "N": N, "nnz": m.nnz, "blocks": nb,
                    "block_fill": round(m.nnz / (128 * max(nb, 1)), 4), "kernel": args.kernel,
                    "schedule": f"{plan.policy[0]}:{plan.policy[1]}", "seed": m.seed,
-                   "conversion_s": round(conv_s, 3), "meta": m.meta},
+                   "conversion_s": round(conv_s, 3), "meta": m.meta,
+                   "knobs": {"depth": args.depth or 2, "tile_b": args.tile_b, "wg_cols": args.wg_cols or 128,
+                             "grid_order": args.grid_order or 1, "windows_per_wave": args.wpw or 1}},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "algorithmic_bytes": int(ab), "compulsory_bytes": int(compulsory),

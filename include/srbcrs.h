@@ -134,6 +134,41 @@ int srbcrs_plan_set_schedule(srbcrs_plan *plan, const char *policy, int32_t para
 int srbcrs_run(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int64_t ldb,
                float *d_C, int64_t ldc, int64_t c_rows, void *stream);
 
+/* Launch knobs of the SR-BCRS kernels (template parameters; each maps a
+ * knob of the reference's strategy schema, strategy_agent.py:81-130):
+ *   depth        blocks in flight per wave: 2, 4 or 8 (0 = 2); the
+ *                software-pipeline depth (the reference's 2-buffer,
+ *                3-stage pipeline, sr_bcrs_ops.py:684-708); indices are
+ *                fetched one further ring ahead (its stage shift);
+ *   tile_b       16, 32 or 64: caps the columns one lane group covers per
+ *                MFMA sweep (16 * vector width) (0 = widest legal); the
+ *                reference's N tile (SRBCRSSpMM_kernel.cu:435-475);
+ *   wg_cols      columns per workgroup, a power of two in 64..512
+ *                (0 = 128);
+ *   grid_order   0 = default (chunk-major), 1 = chunk-major: one column
+ *                chunk of every window before the next chunk (narrower B
+ *                working set per XCD), 2 = window-major;
+ *   windows_per_wave  "row" schedule: consecutive row windows one wave
+ *                streams through its register ring (0 = 1), in [0, 4096].
+ * Values outside these sets are rejected.  Every setting yields the same
+ * bits: the per-element accumulation order does not depend on them. */
+typedef struct srbcrs_run_opts {
+  int32_t depth;
+  int32_t tile_b;
+  int32_t wg_cols;
+  int32_t grid_order;
+  int32_t windows_per_wave;
+} srbcrs_run_opts;
+
+#define SRBCRS_GRID_DEFAULT 0
+#define SRBCRS_GRID_CHUNK_MAJOR 1
+#define SRBCRS_GRID_WINDOW_MAJOR 2
+
+/* srbcrs_run with explicit knobs (opts NULL = defaults). */
+int srbcrs_run_ex(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int64_t ldb,
+                  float *d_C, int64_t ldc, int64_t c_rows, const srbcrs_run_opts *opts,
+                  void *stream);
+
 /* ---- CSR fallback for low block density: C[r, :] = sum_e val[e] *
  * B[col[e], :], fp32, edge order.  The arithmetic of csr_spmm_value_kernel
  * (SRK:66-105), one wave64 per row.  max_col (host-known bound on colind,

@@ -86,14 +86,24 @@ class Plan:
         """nnz / (blocks * blk_h * blk_w): the stored-value density."""
         return self.nnz / max(1, self.total_blocks * self.blk_h * self.blk_w)
 
-    def run(self, dense: Tensor, out: Optional[Tensor] = None) -> Tensor:
-        """out[:num_nodes] = A @ dense on the current stream."""
+    def run(self, dense: Tensor, out: Optional[Tensor] = None, depth: int = 0, tile_b: int = 0, wg_cols: int = 0,
+            grid_order: int = 0, windows_per_wave: int = 0) -> Tensor:
+        """out[:num_nodes] = A @ dense on the current stream.  The keyword
+        knobs are the kernel template parameters (srbcrs_run_opts; 0 =
+        default; grid_order 1 = chunk-major, 2 = window-major)."""
         if out is None:
             out = torch.empty((self.num_nodes, dense.shape[1]), dtype=torch.float32, device=dense.device)
+        if dense.dtype != torch.float32 or out.dtype != torch.float32:
+            raise RuntimeError("dense and out must be float32")
+        if dense.dim() != 2 or dense.stride(1) != 1 or out.dim() != 2 or out.stride(1) != 1:
+            raise RuntimeError("dense and out must be row-major 2-D")
+        if out.shape[1] != dense.shape[1]:
+            raise RuntimeError("out and dense must have the same number of columns")
+        opts = _capi.RunOpts(int(depth), int(tile_b), int(wg_cols), int(grid_order), int(windows_per_wave))
         with torch.cuda.device(self.device):
-            _capi.check(_capi.lib().srbcrs_run(self._h, dense.data_ptr(), int(dense.shape[0]), int(dense.shape[1]),
-                                               int(dense.stride(0)), out.data_ptr(), int(out.stride(0)),
-                                               int(out.shape[0]), _stream_handle(self.device)))
+            _capi.check(_capi.lib().srbcrs_run_ex(self._h, dense.data_ptr(), int(dense.shape[0]), int(dense.shape[1]),
+                                                  int(dense.stride(0)), out.data_ptr(), int(out.stride(0)),
+                                                  int(out.shape[0]), ctypes.byref(opts), _stream_handle(self.device)))
         return out
 
     def close(self) -> None:

@@ -26,7 +26,7 @@ EXPORTS = (
     "srbcrs_plan_create", "srbcrs_plan_destroy", "srbcrs_plan_get", "srbcrs_plan_write_edges",
     "srbcrs_plan_export_index",
     "srbcrs_schedule_build", "srbcrs_schedule_info", "srbcrs_schedule_export", "srbcrs_schedule_destroy",
-    "srbcrs_plan_set_schedule", "srbcrs_run", "srbcrs_csr_spmm",
+    "srbcrs_plan_set_schedule", "srbcrs_run", "srbcrs_run_ex", "srbcrs_csr_spmm",
 )
 
 _i32p = ctypes.POINTER(ctypes.c_int32)
@@ -51,6 +51,11 @@ class PlanDesc(ctypes.Structure):
         ("d_sidx", ctypes.c_void_p),
         ("d_val", ctypes.c_void_p),
     ]
+
+
+class RunOpts(ctypes.Structure):
+    _fields_ = [("depth", ctypes.c_int32), ("tile_b", ctypes.c_int32), ("wg_cols", ctypes.c_int32),
+                ("grid_order", ctypes.c_int32), ("windows_per_wave", ctypes.c_int32)]
 
 
 class SrbcrsError(RuntimeError):
@@ -91,6 +96,8 @@ def lib() -> ctypes.CDLL:
         "srbcrs_schedule_destroy": ([_vp], None),
         "srbcrs_plan_set_schedule": ([_vp, ctypes.c_char_p, _i32], ctypes.c_int),
         "srbcrs_run": ([_vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp], ctypes.c_int),
+        "srbcrs_run_ex": ([_vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64, ctypes.POINTER(RunOpts), _vp],
+                          ctypes.c_int),
         "srbcrs_csr_spmm": ([_vp, _vp, _vp, _i32, _i64, _i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp],
                             ctypes.c_int),
     }

@@ -645,7 +645,32 @@ int srbcrs_plan_set_schedule(srbcrs_plan* plan, const char* policy, int32_t para
 
 int srbcrs_run(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int64_t ldb, float* d_C,
                int64_t ldc, int64_t c_rows, void* stream) {
+  return srbcrs_run_ex(plan, d_B, K, N, ldb, d_C, ldc, c_rows, nullptr, stream);
+}
+
+int srbcrs_run_ex(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int64_t ldb,
+                  float* d_C, int64_t ldc, int64_t c_rows, const srbcrs_run_opts* opts,
+                  void* stream) {
   return guarded([&] {
+    srbcrs::RunOpts ro;
+    int max_vec = 4;
+    if (opts) {
+      if (opts->depth != 0 && opts->depth != 2 && opts->depth != 4 && opts->depth != 8)
+        fail(SRBCRS_EINVAL, "depth must be 0, 2, 4 or 8 (got %d)", opts->depth);
+      if (opts->tile_b != 0 && opts->tile_b != 16 && opts->tile_b != 32 && opts->tile_b != 64)
+        fail(SRBCRS_EINVAL, "tile_b must be 0, 16, 32 or 64 (got %d)", opts->tile_b);
+      if (opts->wg_cols != 0 && (opts->wg_cols < 64 || opts->wg_cols > 512 || (opts->wg_cols & (opts->wg_cols - 1))))
+        fail(SRBCRS_EINVAL, "wg_cols must be 0 or a power of two in [64, 512] (got %d)", opts->wg_cols);
+      if (opts->grid_order < 0 || opts->grid_order > 2)
+        fail(SRBCRS_EINVAL, "grid_order must be 0, 1 or 2 (got %d)", opts->grid_order);
+      if (opts->depth) ro.depth = opts->depth;
+      if (opts->wg_cols) ro.wg_cols = opts->wg_cols;
+      if (opts->grid_order) ro.chunk_major = opts->grid_order == SRBCRS_GRID_CHUNK_MAJOR ? 1 : 0;
+      if (opts->windows_per_wave < 0 || opts->windows_per_wave > 4096)
+        fail(SRBCRS_EINVAL, "windows_per_wave must be in [0, 4096] (got %d)", opts->windows_per_wave);
+      ro.windows_per_wave = opts->windows_per_wave ? opts->windows_per_wave : 1;
+      if (opts->tile_b) max_vec = opts->tile_b / 16;
+    }
     if (!plan) fail(SRBCRS_EINVAL, "plan is NULL");
     if (plan->blk_h != 16 || plan->blk_w != 8)
       fail(SRBCRS_EINVAL, "srbcrs_run supports 16x8 plans (got %dx%d)", plan->blk_h, plan->blk_w);
@@ -665,15 +690,14 @@ int srbcrs_run(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int64_
       fail(SRBCRS_EINVAL, "B / C must be 4-byte aligned");
     hipStream_t st = static_cast<hipStream_t>(stream);
     // vector width: the widest of 4/2/1 that N, ldb, ldc and the pointers allow
-    int vec = 4;
+    int vec = max_vec;
     while (vec > 1 && ((N % (16 * vec)) || (ldb % vec) || (ldc % vec) ||
                        (reinterpret_cast<uintptr_t>(d_B) % (4 * vec)) ||
                        (reinterpret_cast<uintptr_t>(d_C) % (4 * vec))))
       vec /= 2;
+    srbcrs::StreamArgs a{d_B, d_C, nullptr, plan->d_sidx, plan->d_val, plan->num_nodes, (int)N, ldb, ldc};
     if (plan->sched.policy == "row") {
-      srbcrs::RowArgs a{d_B, d_C, plan->d_soff, plan->d_sidx, plan->d_val,
-                        plan->num_nodes, (int)N, plan->Mo, ldb, ldc};
-      hip_check(srbcrs::launch_row(a, vec, st), "launch spmm16x8_row");
+      hip_check(srbcrs::launch_row(a, plan->d_soff, plan->Mo, vec, ro, st), "launch spmm16x8_stream(row)");
       return;
     }
     const Schedule& s = plan->sched;
@@ -685,11 +709,10 @@ int srbcrs_run(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int64_
       plan->d_partial = dev_alloc<float>(need);
       plan->partial_cap = need;
     }
-    srbcrs::TaskArgs ta{d_B, d_C, plan->d_partial, plan->d_sidx, plan->d_val,
-                        plan->d_group_off, plan->d_task_begin, plan->d_task_end,
-                        plan->d_task_window, plan->d_task_slot,
-                        (int)s.group_off.size() - 1, plan->num_nodes, (int)N, ldb, ldc};
-    hip_check(srbcrs::launch_tasks(ta, vec, st), "launch spmm16x8_tasks");
+    a.partial = plan->d_partial;
+    srbcrs::TaskTable tt{plan->d_group_off, plan->d_task_begin, plan->d_task_end, plan->d_task_window,
+                         plan->d_task_slot, (int)s.group_off.size() - 1};
+    hip_check(srbcrs::launch_tasks(a, tt, vec, ro, st), "launch spmm16x8_stream(tasks)");
     srbcrs::ReduceArgs ra{plan->d_partial, d_C, plan->d_red_window, plan->d_red_slot_off,
                           (int)s.red_window.size(), plan->num_nodes, (int)N, ldc};
     hip_check(srbcrs::launch_reduce(ra, vec, st), "launch segment_reduce");

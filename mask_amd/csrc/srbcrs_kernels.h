@@ -6,32 +6,33 @@
 namespace srbcrs {
 
 constexpr int kNumXcd = 8;   // MI355X: 8 XCDs, 32 CUs each
-constexpr int kDepth = 4;    // blocks in flight per wave in the SR-BCRS kernels
 
-struct RowArgs {
+// Launch knobs (template / runtime parameters of the SR-BCRS kernels).
+struct RunOpts {
+  int depth = 2;        // blocks in flight per wave: 2, 4 or 8
+  int wg_cols = 128;    // columns per workgroup (0 = up to 4 waves x 128)
+  int chunk_major = 1;  // grid order: 0 window-major, 1 chunk-major
+  int windows_per_wave = 1;  // row schedule: consecutive windows streamed per wave
+};
+
+// Operands shared by every SR-BCRS launch.
+struct StreamArgs {
   const float* B;
   float* C;
-  const int* soff;
+  float* partial;   // partial tiles of split schedules (may be null for "row")
   const int* sidx;
   const float* val;
-  int M, N, Mo;
+  int M, N;
   int64_t ldb, ldc;
 };
 
-struct TaskArgs {
-  const float* B;
-  float* C;
-  float* partial;
-  const int* sidx;
-  const float* val;
+struct TaskTable {
   const int* group_off;
   const int* task_begin;
   const int* task_end;
   const int* task_window;
   const int* task_slot;
   int n_groups;
-  int M, N;
-  int64_t ldb, ldc;
 };
 
 struct ReduceArgs {
@@ -54,8 +55,10 @@ struct CsrArgs {
   int64_t ldb, ldc;
 };
 
-hipError_t launch_row(const RowArgs& a, int vec, hipStream_t st);
-hipError_t launch_tasks(const TaskArgs& a, int vec, hipStream_t st);
+hipError_t launch_row(const StreamArgs& a, const int* soff, int Mo, int vec, const RunOpts& o,
+                      hipStream_t st);
+hipError_t launch_tasks(const StreamArgs& a, const TaskTable& t, int vec, const RunOpts& o,
+                        hipStream_t st);
 hipError_t launch_reduce(const ReduceArgs& a, int vec, hipStream_t st);
 hipError_t launch_csr(const CsrArgs& a, int vec, hipStream_t st);
 

@@ -158,72 +158,132 @@ __device__ __forceinline__ void store_tile(const f4 (&acc)[G][VEC], float* __res
   }
 }
 
-// One workgroup = WAVES waves on one (row window, column chunk); a column
-// chunk is WAVES * 16*VEC*G columns.  Grid is 1-D over Mo * n_chunks.
-template <int VEC, int G, int WAVES, int DEPTH>
-__global__ __launch_bounds__(64 * WAVES) void spmm16x8_row(
-    const float* __restrict__ B, float* __restrict__ C, const int* __restrict__ soff,
+// Task sources.  A task is a block range [begin, end) of one row window
+// whose 16-row result goes straight into C (slot < 0) or into partial slot
+// `slot` for the segment reduction.  A group is a run of consecutive tasks
+// with contiguous block ranges, processed by one wave per column chunk.
+
+// Row schedule: task t = row window t, groups of `wpw` consecutive windows.
+struct RowTasks {
+  const int* __restrict__ soff;
+  int Mo;
+  int wpw;
+  __device__ __forceinline__ void group(int g, int& t0, int& t1) const {
+    t0 = g * wpw;
+    t1 = t0 + wpw < Mo ? t0 + wpw : Mo;
+  }
+  __device__ __forceinline__ int64_t begin(int t) const { return soff[t]; }
+  __device__ __forceinline__ int64_t end(int t) const { return soff[t + 1]; }
+  __device__ __forceinline__ int window(int t) const { return t; }
+  __device__ __forceinline__ int slot(int) const { return -1; }
+};
+
+// Table schedule (split / strict_lb / multi_bind) built on the host.
+struct TableTasks {
+  const int* __restrict__ group_off;
+  const int* __restrict__ task_begin;
+  const int* __restrict__ task_end;
+  const int* __restrict__ task_window;
+  const int* __restrict__ task_slot;
+  __device__ __forceinline__ void group(int g, int& t0, int& t1) const {
+    t0 = group_off[g];
+    t1 = group_off[g + 1];
+  }
+  __device__ __forceinline__ int64_t begin(int t) const { return task_begin[t]; }
+  __device__ __forceinline__ int64_t end(int t) const { return task_end[t]; }
+  __device__ __forceinline__ int window(int t) const { return task_window[t]; }
+  __device__ __forceinline__ int slot(int t) const { return task_slot[t]; }
+};
+
+template <class Src, int VEC, int G>
+__device__ __forceinline__ void flush_task(const Src& src, int t, f4 (&acc)[G][VEC],
+                                           float* __restrict__ C, float* __restrict__ partial,
+                                           int M, int64_t ldc, int col0, int lane) {
+  const int slot = src.slot(t);
+  if (slot < 0)
+    store_tile<VEC, G>(acc, C, (int64_t)src.window(t) * 16, M, ldc, col0, lane);
+  else
+    store_tile<VEC, G>(acc, partial, (int64_t)slot * 16, (int64_t)(slot + 1) * 16, ldc, col0, lane);
+#pragma unroll
+  for (int g = 0; g < G; ++g)
+#pragma unroll
+    for (int s = 0; s < VEC; ++s) acc[g][s] = f4{0.f, 0.f, 0.f, 0.f};
+}
+
+// One workgroup = WAVES waves on one (task group, column chunk); a column
+// chunk is WAVES * 16*VEC*G columns.  The grid is 1-D over n_groups *
+// n_chunks, in group-major order (all chunks of a group adjacent) or
+// chunk-major order (one column chunk of every group first: the B rows a
+// chunk touches are narrower, so neighbouring windows' shared rows stay in
+// L2).  Each wave streams the group's blocks through one DEPTH-deep register
+// ring without draining it at task boundaries: the accumulator tile is
+// flushed and cleared when the block index crosses a task's end, so short
+// windows (banded matrices) keep the loads of the next windows in flight.
+// Every output element has exactly one writer per launch: no atomics.
+template <class Src, int VEC, int G, int WAVES, int DEPTH>
+__global__ __launch_bounds__(64 * WAVES) void spmm16x8_stream(
+    Src src, const float* __restrict__ B, float* __restrict__ C, float* __restrict__ partial,
     const int* __restrict__ sidx, const float* __restrict__ val, int M, int N, int64_t ldb,
-    int64_t ldc, int n_chunks) {
+    int64_t ldc, int n_chunks, int chunk_major) {
   constexpr int WCOLS = 16 * VEC * G;
   const int64_t nwg = (int64_t)gridDim.x;
   const int64_t lid = xcd_remap(blockIdx.x, nwg);
-  const int w = (int)(lid / n_chunks);
-  const int chunk = (int)(lid % n_chunks);
+  const int64_t n_units = nwg / n_chunks;
+  const int grp = (int)(chunk_major ? lid % n_units : lid / n_chunks);
+  const int chunk = (int)(chunk_major ? lid / n_units : lid % n_chunks);
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int wcol = (chunk * WAVES + wave) * WCOLS;
   if (wcol >= N) return;
   const int col0 = wcol + VEC * (lane & 15);
+  int t0, t1;
+  src.group(grp, t0, t1);
+  if (t0 >= t1) return;
   f4 acc[G][VEC];
 #pragma unroll
   for (int g = 0; g < G; ++g)
 #pragma unroll
     for (int s = 0; s < VEC; ++s) acc[g][s] = f4{0.f, 0.f, 0.f, 0.f};
-  const int64_t b0 = soff[w], b1 = soff[w + 1];
-  if (b0 < b1) accumulate_blocks<VEC, G, DEPTH>(acc, B, sidx, val, b0, b1, ldb, col0, lane);
-  store_tile<VEC, G>(acc, C, (int64_t)w * 16, M, ldc, col0, lane);
-}
-
-// Task-mapped variant: workgroup group g runs tasks [group_off[g],
-// group_off[g+1]); task t accumulates blocks [task_begin[t], task_end[t]) of
-// window task_window[t] and writes the 16-row tile either straight into C
-// (task_slot[t] < 0) or into partial slot task_slot[t] (16 x N, row stride
-// ldc) for the segment-reduce kernel.  No atomics: every output element has
-// exactly one writer per launch.
-template <int VEC, int G, int WAVES, int DEPTH>
-__global__ __launch_bounds__(64 * WAVES) void spmm16x8_tasks(
-    const float* __restrict__ B, float* __restrict__ C, float* __restrict__ partial,
-    const int* __restrict__ sidx, const float* __restrict__ val,
-    const int* __restrict__ group_off, const int* __restrict__ task_begin,
-    const int* __restrict__ task_end, const int* __restrict__ task_window,
-    const int* __restrict__ task_slot, int M, int N, int64_t ldb, int64_t ldc, int n_chunks) {
-  constexpr int WCOLS = 16 * VEC * G;
-  const int64_t nwg = (int64_t)gridDim.x;
-  const int64_t lid = xcd_remap(blockIdx.x, nwg);
-  const int grp = (int)(lid / n_chunks);
-  const int chunk = (int)(lid % n_chunks);
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int wcol = (chunk * WAVES + wave) * WCOLS;
-  if (wcol >= N) return;
-  const int col0 = wcol + VEC * (lane & 15);
-  const int t0 = group_off[grp], t1 = group_off[grp + 1];
-  for (int t = t0; t < t1; ++t) {
-    f4 acc[G][VEC];
+  const int64_t bs = src.begin(t0), be = src.end(t1 - 1);
+  int t = t0;
+  int64_t tend = src.end(t0);
+  if (bs < be) {
+    const int k = lane >> 4;
+    const int i = lane & 15;
+    const int a_off = swz16x8(8 * i + 2 * k);
+    Frag<VEC, G> f[DEPTH];
+    int2 idx[DEPTH];
+    const int64_t last = be - 1;
 #pragma unroll
-    for (int g = 0; g < G; ++g)
+    for (int d = 0; d < DEPTH; ++d) {
+      const int64_t blk = bs + d < last ? bs + d : last;
+      const int2 rows = *reinterpret_cast<const int2*>(sidx + blk * 8 + 2 * k);
+      load_frag<VEC, G>(f[d], B, val, blk, rows, a_off, ldb, col0);
+      const int64_t nblk = bs + DEPTH + d < last ? bs + DEPTH + d : last;
+      idx[d] = *reinterpret_cast<const int2*>(sidx + nblk * 8 + 2 * k);
+    }
+    for (int64_t base = bs; base < be; base += DEPTH) {
 #pragma unroll
-      for (int s = 0; s < VEC; ++s) acc[g][s] = f4{0.f, 0.f, 0.f, 0.f};
-    const int64_t b0 = task_begin[t], b1 = task_end[t];
-    if (b0 < b1) accumulate_blocks<VEC, G, DEPTH>(acc, B, sidx, val, b0, b1, ldb, col0, lane);
-    const int slot = task_slot[t];
-    if (slot < 0) {
-      store_tile<VEC, G>(acc, C, (int64_t)task_window[t] * 16, M, ldc, col0, lane);
-    } else {
-      store_tile<VEC, G>(acc, partial, (int64_t)slot * 16, (int64_t)(slot + 1) * 16, ldc, col0, lane);
+      for (int d = 0; d < DEPTH; ++d) {
+        const int64_t blk = base + d;
+        if (blk < be) {
+          while (blk >= tend) {   // crossed into the next task (empty tasks flush zeros)
+            flush_task<Src, VEC, G>(src, t, acc, C, partial, M, ldc, col0, lane);
+            ++t;
+            tend = src.end(t);
+          }
+          mma_frag<VEC, G>(f[d], acc);
+        }
+        const int64_t nblk = blk + DEPTH;
+        if (nblk < be) {
+          load_frag<VEC, G>(f[d], B, val, nblk, idx[d], a_off, ldb, col0);
+          const int64_t nn = nblk + DEPTH < last ? nblk + DEPTH : last;
+          idx[d] = *reinterpret_cast<const int2*>(sidx + nn * 8 + 2 * k);
+        }
+      }
     }
   }
+  for (; t < t1; ++t) flush_task<Src, VEC, G>(src, t, acc, C, partial, M, ldc, col0, lane);
 }
 
 // out rows of window red_window[i] = sum over slots [red_slot_off[i],
@@ -300,72 +360,73 @@ __global__ __launch_bounds__(256) void csr_spmm_rowwave(
 // ---------------------------------------------------------------------------
 // Host launchers.
 
-static int pick_waves(int N, int wcols) {
+static int pick_waves(int N, int wcols, int wg_cols) {
+  int cap = 4;
+  if (wg_cols > 0) cap = wg_cols / wcols < 1 ? 1 : wg_cols / wcols;
   int w = (N + wcols - 1) / wcols;
+  if (w > cap) w = cap;
   return w >= 4 ? 4 : (w >= 2 ? 2 : 1);
 }
 
-template <int VEC, int G, int DEPTH>
-static hipError_t launch_row_vg(const RowArgs& a, hipStream_t st) {
+template <class Src, int VEC, int G, int DEPTH>
+static hipError_t launch_vg(const Src& src, int n_groups, const StreamArgs& a, const RunOpts& o,
+                            hipStream_t st) {
   constexpr int WCOLS = 16 * VEC * G;
-  const int waves = pick_waves(a.N, WCOLS);
+  const int waves = pick_waves(a.N, WCOLS, o.wg_cols);
   const int chunk_cols = waves * WCOLS;
   const int n_chunks = (a.N + chunk_cols - 1) / chunk_cols;
-  const int64_t nwg = (int64_t)a.Mo * n_chunks;
+  const int64_t nwg = (int64_t)n_groups * n_chunks;
   if (nwg == 0) return hipSuccess;
+  if (nwg > INT32_MAX) return hipErrorInvalidConfiguration;
   dim3 grid((unsigned)nwg);
+#define SRBCRS_LAUNCH(W)                                                                        \
+  hipLaunchKernelGGL((spmm16x8_stream<Src, VEC, G, W, DEPTH>), grid, dim3(64 * W), 0, st, src, \
+                     a.B, a.C, a.partial, a.sidx, a.val, a.M, a.N, a.ldb, a.ldc, n_chunks,      \
+                     o.chunk_major)
   switch (waves) {
-    case 4:
-      hipLaunchKernelGGL((spmm16x8_row<VEC, G, 4, DEPTH>), grid, dim3(256), 0, st, a.B, a.C, a.soff,
-                         a.sidx, a.val, a.M, a.N, a.ldb, a.ldc, n_chunks);
-      break;
-    case 2:
-      hipLaunchKernelGGL((spmm16x8_row<VEC, G, 2, DEPTH>), grid, dim3(128), 0, st, a.B, a.C, a.soff,
-                         a.sidx, a.val, a.M, a.N, a.ldb, a.ldc, n_chunks);
-      break;
-    default:
-      hipLaunchKernelGGL((spmm16x8_row<VEC, G, 1, DEPTH>), grid, dim3(64), 0, st, a.B, a.C, a.soff,
-                         a.sidx, a.val, a.M, a.N, a.ldb, a.ldc, n_chunks);
-      break;
+    case 4: SRBCRS_LAUNCH(4); break;
+    case 2: SRBCRS_LAUNCH(2); break;
+    default: SRBCRS_LAUNCH(1); break;
   }
+#undef SRBCRS_LAUNCH
   return hipGetLastError();
 }
 
-template <int VEC, int G, int DEPTH>
-static hipError_t launch_tasks_vg(const TaskArgs& a, hipStream_t st) {
-  constexpr int WCOLS = 16 * VEC * G;
-  const int waves = pick_waves(a.N, WCOLS);
-  const int chunk_cols = waves * WCOLS;
-  const int n_chunks = (a.N + chunk_cols - 1) / chunk_cols;
-  const int64_t nwg = (int64_t)a.n_groups * n_chunks;
-  if (nwg == 0) return hipSuccess;
-  dim3 grid((unsigned)nwg);
-#define SRBCRS_LAUNCH_TASKS(W)                                                                   \
-  hipLaunchKernelGGL((spmm16x8_tasks<VEC, G, W, DEPTH>), grid, dim3(64 * W), 0, st, a.B, a.C,   \
-                     a.partial, a.sidx, a.val, a.group_off, a.task_begin, a.task_end,            \
-                     a.task_window, a.task_slot, a.M, a.N, a.ldb, a.ldc, n_chunks)
-  switch (waves) {
-    case 4: SRBCRS_LAUNCH_TASKS(4); break;
-    case 2: SRBCRS_LAUNCH_TASKS(2); break;
-    default: SRBCRS_LAUNCH_TASKS(1); break;
+template <class Src, int DEPTH>
+static hipError_t launch_d(const Src& src, int n_groups, const StreamArgs& a, int vec,
+                           const RunOpts& o, hipStream_t st) {
+  if (vec == 4)
+    return (a.N % 128 == 0 && o.wg_cols != 64) ? launch_vg<Src, 4, 2, DEPTH>(src, n_groups, a, o, st)
+                                              : launch_vg<Src, 4, 1, DEPTH>(src, n_groups, a, o, st);
+  if (vec == 2) return launch_vg<Src, 2, 1, DEPTH>(src, n_groups, a, o, st);
+  return launch_vg<Src, 1, 1, DEPTH>(src, n_groups, a, o, st);
+}
+
+template <class Src>
+static hipError_t launch_src(const Src& src, int n_groups, const StreamArgs& a, int vec,
+                             const RunOpts& o, hipStream_t st) {
+  switch (o.depth) {
+    case 2: return launch_d<Src, 2>(src, n_groups, a, vec, o, st);
+    case 8: return launch_d<Src, 8>(src, n_groups, a, vec, o, st);
+    default: return launch_d<Src, 4>(src, n_groups, a, vec, o, st);
   }
-#undef SRBCRS_LAUNCH_TASKS
-  return hipGetLastError();
 }
 
 // vec (4, 2 or 1; 16*vec divides N) is chosen by the caller from N, the
 // leading dimensions and pointer alignment; G = 2 column groups per wave when
-// the 128-column wave tile divides N.
-hipError_t launch_row(const RowArgs& a, int vec, hipStream_t st) {
-  if (vec == 4) return a.N % 128 == 0 ? launch_row_vg<4, 2, kDepth>(a, st) : launch_row_vg<4, 1, kDepth>(a, st);
-  if (vec == 2) return launch_row_vg<2, 1, kDepth>(a, st);
-  return launch_row_vg<1, 1, kDepth>(a, st);
+// the 128-column wave tile divides N (and 64-column workgroups are not
+// requested); DEPTH = blocks in flight per wave.
+hipError_t launch_row(const StreamArgs& a, const int* soff, int Mo, int vec, const RunOpts& o,
+                      hipStream_t st) {
+  const int wpw = o.windows_per_wave > 0 ? o.windows_per_wave : 1;
+  RowTasks src{soff, Mo, wpw};
+  return launch_src(src, (Mo + wpw - 1) / wpw, a, vec, o, st);
 }
 
-hipError_t launch_tasks(const TaskArgs& a, int vec, hipStream_t st) {
-  if (vec == 4) return a.N % 128 == 0 ? launch_tasks_vg<4, 2, kDepth>(a, st) : launch_tasks_vg<4, 1, kDepth>(a, st);
-  if (vec == 2) return launch_tasks_vg<2, 1, kDepth>(a, st);
-  return launch_tasks_vg<1, 1, kDepth>(a, st);
+hipError_t launch_tasks(const StreamArgs& a, const TaskTable& t, int vec, const RunOpts& o,
+                        hipStream_t st) {
+  TableTasks src{t.group_off, t.task_begin, t.task_end, t.task_window, t.task_slot};
+  return launch_src(src, t.n_groups, a, vec, o, st);
 }
 
 hipError_t launch_reduce(const ReduceArgs& a, int vec, hipStream_t st) {

@@ -166,3 +166,26 @@ def test_csr_fallback(gpu):
                        torch.from_numpy(values).cuda(), torch.from_numpy(B).cuda(), M)
         torch.cuda.synchronize()
         assert_gate(gate(out.cpu().numpy(), rowptr, colind, values, B, M))
+
+
+def test_knobs_are_bitwise_invariant(gpu):
+    """Depth, tile_b, workgroup width, grid order and windows-per-wave change
+    only the mapping, never the per-element accumulation order: every
+    combination reproduces the default result bit for bit."""
+    torch = _torch()
+    import itertools
+    M, K, N = 333, 900, 256
+    rowptr, colind, values = random_csr(M, K, 0.02, seed=31, empty_rows=0.3, heavy_rows=3, heavy_len=400)
+    B = np.random.default_rng(4).uniform(-1, 1, (K, N)).astype(np.float32)
+    _say("knobs", M, K, N)
+    ref, plan = _run_plan(rowptr, colind, values, M, B)
+    dB = torch.from_numpy(B).cuda()
+    for depth, tile_b, wgc, go, wpw in itertools.product([2, 4, 8], [0, 16, 32], [0, 64, 256], [1, 2], [1, 3, 16]):
+        out = plan.run(dB, depth=depth, tile_b=tile_b, wg_cols=wgc, grid_order=go, windows_per_wave=wpw)
+        assert np.array_equal(out.cpu().numpy(), ref), (depth, tile_b, wgc, cm, wpw)
+    for pol in (("split", 0), ("strict_lb", 7), ("multi_bind", 0)):
+        plan.set_schedule(*pol)
+        base = plan.run(dB).cpu().numpy()
+        for depth, wgc, go in itertools.product([4, 8], [0, 64, 512], [1, 2]):
+            out = plan.run(dB, depth=depth, wg_cols=wgc, grid_order=go)
+            assert np.array_equal(out.cpu().numpy(), base), (pol, depth, wgc, go)
