@@ -94,6 +94,12 @@ int srbcrs_plan_export_index(const srbcrs_plan *plan, int32_t *d_row_window_offs
                              int64_t row_window_offset_len, int32_t *d_tcblocktile_id,
                              int64_t tcblocktile_id_len, void *stream);
 
+/* Copy the plan's swizzled block values (blk_h * blk_w * total_blocks
+ * floats, the reference's tcblock_val, SRK:329-330) into a caller-owned
+ * device buffer.  A short buffer is an error. */
+int srbcrs_plan_export_values(const srbcrs_plan *plan, float *d_val, int64_t val_len,
+                              void *stream);
+
 /* ---- Execution schedules (host logic).  policy:
  *   "row"        one task per row window, written straight into C
  *                (the plain kernel's mapping, kernel.inc:1590-1700);
@@ -123,11 +129,12 @@ void srbcrs_schedule_destroy(srbcrs_schedule *s);
  * tables to the plan's device. */
 int srbcrs_plan_set_schedule(srbcrs_plan *plan, const char *policy, int32_t param);
 
-/* ---- SpMM.  C[0:c_rows, 0:N] = A * B with A the plan's matrix
+/* ---- SpMM.  C[0:c_rows, 0:N] = A * B with A the plan's matrix (16x8 or
+ * 32x32 blocks)
  * (replaces run_spmm_srcfp32_srbcrs, SRK:395-557, pybind run_SRBCRS_16x8 /
  * run_SRBCRS and the *_balance aliases, SRC:120-192).  B is K x N
  * row-major with leading dimension ldb, C is c_rows x N with ldc.
- * Requirements: 16 x 8 plan, N % 16 == 0, K > max column, c_rows >=
+ * Requirements: N % 16 == 0, K > max column, c_rows >=
  * num_nodes (rows beyond num_nodes are not written).  Every row
  * < num_nodes of C is overwritten (zeros for empty windows).  Schedules
  * other than "row" use a plan-owned partial buffer grown on demand. */

@@ -106,6 +106,15 @@ class Plan:
                                                   int(out.shape[0]), ctypes.byref(opts), _stream_handle(self.device)))
         return out
 
+    def block_values(self) -> Tensor:
+        """The swizzled block values on the device (a copy)."""
+        n = self.total_blocks * self.blk_h * self.blk_w
+        out = torch.empty(n, dtype=torch.float32, device=self.device)
+        with torch.cuda.device(self.device):
+            _capi.check(_capi.lib().srbcrs_plan_export_values(self._h, out.data_ptr() if n else None, n,
+                                                              _stream_handle(self.device)))
+        return out
+
     def close(self) -> None:
         if getattr(self, "_h", None):
             _capi.lib().srbcrs_plan_destroy(self._h)
@@ -241,9 +250,6 @@ def _run(dense: Tensor, row_window_offset: Tensor, tcblocktile_id: Tensor, tcblo
                            "Please pad feature dim before run.")
     if entry.plan.total_blocks <= 0:
         raise RuntimeError("SR-BCRS has empty preprocessed blocks; CSR fallback disabled.")
-    if not use_16x8:
-        raise RuntimeError("SR-BCRS 32x32 execution is not available in the gfx950 backend; "
-                           "use preprocess_gpu_16x8 / run_SRBCRS_16x8")
     sched = _schedule_from_exeplan(exeplan)
     entry.plan.set_schedule(*(sched or ("row", 0)))
     out = torch.empty((entry.num_nodes, n), dtype=torch.float32, device=dense.device)

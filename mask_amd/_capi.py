@@ -24,7 +24,7 @@ EXPORTS = (
     "srbcrs_last_error", "srbcrs_version",
     "srbcrs_convert_count", "srbcrs_convert_fill",
     "srbcrs_plan_create", "srbcrs_plan_destroy", "srbcrs_plan_get", "srbcrs_plan_write_edges",
-    "srbcrs_plan_export_index",
+    "srbcrs_plan_export_index", "srbcrs_plan_export_values",
     "srbcrs_schedule_build", "srbcrs_schedule_info", "srbcrs_schedule_export", "srbcrs_schedule_destroy",
     "srbcrs_plan_set_schedule", "srbcrs_run", "srbcrs_run_ex", "srbcrs_csr_spmm",
 )
@@ -90,6 +90,7 @@ def lib() -> ctypes.CDLL:
         "srbcrs_plan_get": ([_vp, ctypes.POINTER(PlanDesc)], ctypes.c_int),
         "srbcrs_plan_write_edges": ([_vp, _vp, _i64, _vp, _i64, _vp, _i64, _vp], ctypes.c_int),
         "srbcrs_plan_export_index": ([_vp, _vp, _i64, _vp, _i64, _vp], ctypes.c_int),
+        "srbcrs_plan_export_values": ([_vp, _vp, _i64, _vp], ctypes.c_int),
         "srbcrs_schedule_build": ([_vp, _i32, ctypes.c_char_p, _i32, ctypes.POINTER(_vp)], ctypes.c_int),
         "srbcrs_schedule_info": ([_vp, _i32p, _i32p, _i32p, _i32p], ctypes.c_int),
         "srbcrs_schedule_export": ([_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp], ctypes.c_int),

@@ -578,6 +578,17 @@ int srbcrs_plan_export_index(const srbcrs_plan* plan, int32_t* d_row_window_offs
   });
 }
 
+int srbcrs_plan_export_values(const srbcrs_plan* plan, float* d_val, int64_t val_len, void* stream) {
+  return guarded([&] {
+    if (!plan) fail(SRBCRS_EINVAL, "plan is NULL");
+    const int64_t n = plan->total * plan->blk_h * plan->blk_w;
+    if (n == 0) return;
+    if (!d_val || val_len < n) fail(SRBCRS_EINVAL, "value buffer too short (%lld < %lld)", (long long)val_len, (long long)n);
+    hip_check(hipMemcpyAsync(d_val, plan->d_val, (size_t)n * 4, hipMemcpyDeviceToDevice, static_cast<hipStream_t>(stream)),
+              "copy values");
+  });
+}
+
 int srbcrs_schedule_build(const int32_t* soff, int32_t row_windows, const char* policy,
                           int32_t param, srbcrs_schedule** out) {
   return guarded([&] {
@@ -672,8 +683,6 @@ int srbcrs_run_ex(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int
       if (opts->tile_b) max_vec = opts->tile_b / 16;
     }
     if (!plan) fail(SRBCRS_EINVAL, "plan is NULL");
-    if (plan->blk_h != 16 || plan->blk_w != 8)
-      fail(SRBCRS_EINVAL, "srbcrs_run supports 16x8 plans (got %dx%d)", plan->blk_h, plan->blk_w);
     int cur = 0;
     hip_check(hipGetDevice(&cur), "hipGetDevice");
     if (cur != plan->device) fail(SRBCRS_ESTATE, "plan lives on device %d, current device is %d", plan->device, cur);
@@ -695,13 +704,14 @@ int srbcrs_run_ex(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int
                        (reinterpret_cast<uintptr_t>(d_B) % (4 * vec)) ||
                        (reinterpret_cast<uintptr_t>(d_C) % (4 * vec))))
       vec /= 2;
-    srbcrs::StreamArgs a{d_B, d_C, nullptr, plan->d_sidx, plan->d_val, plan->num_nodes, (int)N, ldb, ldc};
+    srbcrs::StreamArgs a{d_B, d_C, nullptr, plan->d_sidx, plan->d_val, plan->num_nodes, (int)N, ldb, ldc,
+                         plan->blk_h};
     if (plan->sched.policy == "row") {
-      hip_check(srbcrs::launch_row(a, plan->d_soff, plan->Mo, vec, ro, st), "launch spmm16x8_stream(row)");
+      hip_check(srbcrs::launch_row(a, plan->d_soff, plan->Mo, vec, ro, st), "launch spmm_stream(row)");
       return;
     }
     const Schedule& s = plan->sched;
-    const size_t need = (size_t)s.n_slots * 16 * (size_t)ldc;
+    const size_t need = (size_t)s.n_slots * plan->blk_h * (size_t)ldc;
     if (need > plan->partial_cap) {
       hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
       dev_free(plan->d_partial);
@@ -712,9 +722,9 @@ int srbcrs_run_ex(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int
     a.partial = plan->d_partial;
     srbcrs::TaskTable tt{plan->d_group_off, plan->d_task_begin, plan->d_task_end, plan->d_task_window,
                          plan->d_task_slot, (int)s.group_off.size() - 1};
-    hip_check(srbcrs::launch_tasks(a, tt, vec, ro, st), "launch spmm16x8_stream(tasks)");
+    hip_check(srbcrs::launch_tasks(a, tt, vec, ro, st), "launch spmm_stream(tasks)");
     srbcrs::ReduceArgs ra{plan->d_partial, d_C, plan->d_red_window, plan->d_red_slot_off,
-                          (int)s.red_window.size(), plan->num_nodes, (int)N, ldc};
+                          (int)s.red_window.size(), plan->blk_h, plan->num_nodes, (int)N, ldc};
     hip_check(srbcrs::launch_reduce(ra, vec, st), "launch segment_reduce");
   });
 }

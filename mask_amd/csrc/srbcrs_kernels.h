@@ -9,9 +9,9 @@ constexpr int kNumXcd = 8;   // MI355X: 8 XCDs, 32 CUs each
 
 // Launch knobs (template / runtime parameters of the SR-BCRS kernels).
 struct RunOpts {
-  int depth = 2;        // blocks in flight per wave: 2, 4 or 8
-  int wg_cols = 128;    // columns per workgroup (0 = up to 4 waves x 128)
-  int chunk_major = 1;  // grid order: 0 window-major, 1 chunk-major
+  int depth = 2;             // units in flight per wave: 2, 4 or 8
+  int wg_cols = 128;         // columns per workgroup (0 = up to 4 waves)
+  int chunk_major = 1;       // grid order: 0 window-major, 1 chunk-major
   int windows_per_wave = 1;  // row schedule: consecutive windows streamed per wave
 };
 
@@ -24,6 +24,7 @@ struct StreamArgs {
   const float* val;
   int M, N;
   int64_t ldb, ldc;
+  int blk_h;        // 16 (16x8 blocks) or 32 (32x32 blocks)
 };
 
 struct TaskTable {
@@ -41,6 +42,7 @@ struct ReduceArgs {
   const int* red_window;
   const int* red_slot_off;
   int n_red;
+  int tile_rows;    // rows per window (the block height)
   int M, N;
   int64_t ldc;
 };

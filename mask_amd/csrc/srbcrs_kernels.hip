@@ -1,31 +1,38 @@
-// SR-BCRS 16x8 fp32 SpMM kernels for gfx950 (CDNA4, wave64).
+// SR-BCRS fp32 SpMM kernels for gfx950 (CDNA4, wave64).
 //
-// C[M x N] = A[M x K] * B[K x N], A in SR-BCRS 16x8:
-//   soff[Mo+1]   block offsets per 16-row window
-//   sidx[8*nb]   the 8 B-row (column) indices of each block
-//   val[128*nb]  the block values, 16x8 row-major with CuTe Swizzle<2,2,3>
-//                applied to the offset: pos(r,c) = o ^ ((o & 0x60) >> 3),
-//                o = 8r + c.
-// This is the data the reference's sr_bcrs_spmm_kernel_tf32<16,64,8>
-// consumes (examples/src_fp32/sr_bcrs/testbed/kernel.inc:1590-1700); the
-// arithmetic here is native fp32 MFMA instead of TF32 MMA.
+// C[M x N] = A[M x K] * B[K x N], A in SR-BCRS with BH x BW blocks
+// (16 x 8, or the 32 x 32 base variant):
+//   soff[Mo+1]      block offsets per BH-row window
+//   sidx[BW*nb]     the BW B-row (column) indices of each block
+//   val[BH*BW*nb]   the block values, BH x BW row-major with CuTe
+//                   Swizzle<2,2,3> applied to the offset:
+//                   pos(r,c) = o ^ ((o & 0x60) >> 3), o = BW*r + c.
+// This is the data the reference's sr_bcrs_spmm_kernel_tf32<16,64,8> (and
+// its 32x32 sibling) consumes (examples/src_fp32/sr_bcrs/testbed/
+// kernel.inc:1590-1700); the arithmetic here is native fp32 MFMA instead of
+// TF32 MMA.
+//
+// Units.  A block is BW/8 "units" of 8 columns; unit u of block b has
+// index b*(BW/8) + q and its 8 B-row indices are sidx[8u .. 8u+8), so the
+// kernel walks one contiguous unit sequence for either block shape.
 //
 // MFMA mapping.  v_mfma_f32_16x16x4_f32 (wave64) computes D(16x16) +=
 // A(16x4) * B(4x16) with lane l holding A[l%16][l/16], B[l/16][l%16] and
-// D[4*(l/16)+r][l%16], r = 0..3.  One 16x8 block is two such k-steps; the
-// 8 block columns are split as k-step 0 = {0,2,4,6}, k-step 1 = {1,3,5,7},
-// so lane (i = l%16, k = l/16) needs A[i][2k] and A[i][2k+1].  The swizzle
-// only touches offset bits 2..3, so those two values sit next to each other
-// in memory: one 8-byte load per lane fetches the lane's A fragment.
+// D[4*(l/16)+r][l%16], r = 0..3.  A unit times one 16-row half of the
+// block is two such k-steps; the unit's 8 columns split as k-step 0 =
+// {0,2,4,6}, k-step 1 = {1,3,5,7}, so lane (i = l%16, k = l/16) needs
+// A[i][8q+2k] and A[i][8q+2k+1].  The swizzle only touches offset bits 2..3,
+// so those two values sit next to each other in memory: one 8-byte load per
+// lane and row half fetches the lane's A fragment.
 //
 // Column mapping.  A wave owns 16*VEC*G output columns.  In column group g
 // lane j = l%16 owns columns base + 16*VEC*g + VEC*j + s (s < VEC): one
-// VEC-wide vector load per (B row, g) per lane, VEC MFMAs per k-step and g.
-// For VEC = 4 a wave's B load covers four 256-byte row segments.
+// VEC-wide vector load per (B row, g) per lane, VEC MFMAs per k-step, g and
+// row half.  For VEC = 4 a wave's B load covers four 256-byte row segments.
 //
-// No LDS: every B element is used by exactly one wave (waves of a workgroup
-// split N), so staging through LDS adds no reuse; latency is hidden by a
-// register ring DEPTH blocks deep (indices one more ring ahead).
+// No LDS: every B element is used by exactly one wave (waves split N), so
+// staging through LDS adds no reuse; latency is hidden by a register ring
+// DEPTH units deep, with the B-row indices fetched one ring further ahead.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -47,7 +54,7 @@ template <> __device__ __forceinline__ float vget<1>(const float& v, int) { retu
 template <> __device__ __forceinline__ float vget<2>(const f2& v, int s) { return v[s]; }
 template <> __device__ __forceinline__ float vget<4>(const f4& v, int s) { return v[s]; }
 
-__device__ __forceinline__ int swz16x8(int o) { return o ^ ((o & 0x60) >> 3); }
+__device__ __forceinline__ int swizzle_2_2_3(int o) { return o ^ ((o & 0x60) >> 3); }
 
 // Map the hardware workgroup id to a logical one so that each XCD (the
 // dispatcher deals workgroups round-robin over the 8 XCDs) receives a
@@ -59,20 +66,42 @@ __device__ __forceinline__ int64_t xcd_remap(int64_t id, int64_t n) {
   return x * q + (x < r ? x : r) + t;
 }
 
-template <int VEC, int G>
-struct Frag {
-  typedef typename VecT<VEC>::type V;
-  f2 a;          // A[i][2k], A[i][2k+1]
-  V b0[G];       // B[sidx[2k]][cols of g]
-  V b1[G];       // B[sidx[2k+1]][cols of g]
+// Block geometry: BH x BW blocks, H = BH/16 row halves, Q = BW/8 units.
+template <int BH, int BW>
+struct Shape {
+  static constexpr int H = BH / 16;
+  static constexpr int Q = BW / 8;
+  static constexpr int SIZE = BH * BW;
 };
 
-template <int VEC, int G>
-__device__ __forceinline__ void load_frag(Frag<VEC, G>& f, const float* __restrict__ B,
-                                          const float* __restrict__ val, int64_t blk, int2 rows,
-                                          int a_off, int64_t ldb, int col0) {
+// One unit in flight: the lane's A fragments (one per row half) and its B
+// vectors for the two k-steps.
+template <int H, int VEC, int G>
+struct Frag {
   typedef typename VecT<VEC>::type V;
-  f.a = *reinterpret_cast<const f2*>(val + blk * 128 + a_off);
+  f2 a[H];       // A[16h+i][8q+2k], A[16h+i][8q+2k+1]
+  V b0[G];       // B[sidx[8u+2k]][cols of g]
+  V b1[G];       // B[sidx[8u+2k+1]][cols of g]
+};
+
+template <int BH, int BW, int VEC, int G>
+__device__ __forceinline__ void load_frag(Frag<BH / 16, VEC, G>& f, const float* __restrict__ B,
+                                          const float* __restrict__ val, int64_t unit, int2 rows,
+                                          const int (&a_off)[BW / 8][BH / 16], int64_t ldb,
+                                          int col0) {
+  typedef Shape<BH, BW> S;
+  typedef typename VecT<VEC>::type V;
+  const int64_t blk = unit / S::Q;
+  const int q = (int)(unit % S::Q);
+  const float* vb = val + blk * S::SIZE;
+#pragma unroll
+  for (int h = 0; h < S::H; ++h) {
+    int off = a_off[0][h];
+#pragma unroll
+    for (int qq = 1; qq < S::Q; ++qq)
+      if (q == qq) off = a_off[qq][h];
+    f.a[h] = *reinterpret_cast<const f2*>(vb + off);
+  }
   const float* r0 = B + (int64_t)rows.x * ldb + col0;
   const float* r1 = B + (int64_t)rows.y * ldb + col0;
 #pragma unroll
@@ -82,52 +111,17 @@ __device__ __forceinline__ void load_frag(Frag<VEC, G>& f, const float* __restri
   }
 }
 
-template <int VEC, int G>
-__device__ __forceinline__ void mma_frag(const Frag<VEC, G>& f, f4 (&acc)[G][VEC]) {
+template <int H, int VEC, int G>
+__device__ __forceinline__ void mma_frag(const Frag<H, VEC, G>& f, f4 (&acc)[H][G][VEC]) {
 #pragma unroll
-  for (int g = 0; g < G; ++g) {
+  for (int h = 0; h < H; ++h)
 #pragma unroll
-    for (int s = 0; s < VEC; ++s) {
-      acc[g][s] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a.x, vget<VEC>(f.b0[g], s), acc[g][s], 0, 0, 0);
-      acc[g][s] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a.y, vget<VEC>(f.b1[g], s), acc[g][s], 0, 0, 0);
-    }
-  }
-}
-
-// Accumulate blocks [b0, b1) of one window into acc with a DEPTH-deep ring.
-template <int VEC, int G, int DEPTH>
-__device__ __forceinline__ void accumulate_blocks(f4 (&acc)[G][VEC], const float* __restrict__ B,
-                                                  const int* __restrict__ sidx,
-                                                  const float* __restrict__ val, int64_t b0,
-                                                  int64_t b1, int64_t ldb, int col0, int lane) {
-  const int k = lane >> 4;
-  const int i = lane & 15;
-  const int a_off = swz16x8(8 * i + 2 * k);
-  Frag<VEC, G> f[DEPTH];
-  int2 idx[DEPTH];
-  const int64_t last = b1 - 1;
-  // prologue: indices for blocks b0 .. b0+2*DEPTH-1, data for b0 .. b0+DEPTH-1
+    for (int g = 0; g < G; ++g)
 #pragma unroll
-  for (int d = 0; d < DEPTH; ++d) {
-    int64_t blk = b0 + d < last ? b0 + d : last;
-    int2 rows = *reinterpret_cast<const int2*>(sidx + blk * 8 + 2 * k);
-    load_frag<VEC, G>(f[d], B, val, blk, rows, a_off, ldb, col0);
-    int64_t nblk = b0 + DEPTH + d < last ? b0 + DEPTH + d : last;
-    idx[d] = *reinterpret_cast<const int2*>(sidx + nblk * 8 + 2 * k);
-  }
-  for (int64_t base = b0; base < b1; base += DEPTH) {
-#pragma unroll
-    for (int d = 0; d < DEPTH; ++d) {
-      const int64_t blk = base + d;
-      if (blk < b1) mma_frag<VEC, G>(f[d], acc);
-      const int64_t nblk = blk + DEPTH;
-      if (nblk < b1) {
-        load_frag<VEC, G>(f[d], B, val, nblk, idx[d], a_off, ldb, col0);
-        const int64_t nn = nblk + DEPTH < last ? nblk + DEPTH : last;
-        idx[d] = *reinterpret_cast<const int2*>(sidx + nn * 8 + 2 * k);
+      for (int s = 0; s < VEC; ++s) {
+        acc[h][g][s] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[h].x, vget<VEC>(f.b0[g], s), acc[h][g][s], 0, 0, 0);
+        acc[h][g][s] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[h].y, vget<VEC>(f.b1[g], s), acc[h][g][s], 0, 0, 0);
       }
-    }
-  }
 }
 
 // Store a 16 x (16*VEC*G) accumulator tile.  row0 is the tile's first row in
@@ -159,7 +153,7 @@ __device__ __forceinline__ void store_tile(const f4 (&acc)[G][VEC], float* __res
 }
 
 // Task sources.  A task is a block range [begin, end) of one row window
-// whose 16-row result goes straight into C (slot < 0) or into partial slot
+// whose BH-row result goes straight into C (slot < 0) or into partial slot
 // `slot` for the segment reduction.  A group is a run of consecutive tasks
 // with contiguous block ranges, processed by one wave per column chunk.
 
@@ -195,19 +189,23 @@ struct TableTasks {
   __device__ __forceinline__ int slot(int t) const { return task_slot[t]; }
 };
 
-template <class Src, int VEC, int G>
-__device__ __forceinline__ void flush_task(const Src& src, int t, f4 (&acc)[G][VEC],
+template <class Src, int BH, int VEC, int G>
+__device__ __forceinline__ void flush_task(const Src& src, int t, f4 (&acc)[BH / 16][G][VEC],
                                            float* __restrict__ C, float* __restrict__ partial,
                                            int M, int64_t ldc, int col0, int lane) {
   const int slot = src.slot(t);
-  if (slot < 0)
-    store_tile<VEC, G>(acc, C, (int64_t)src.window(t) * 16, M, ldc, col0, lane);
-  else
-    store_tile<VEC, G>(acc, partial, (int64_t)slot * 16, (int64_t)(slot + 1) * 16, ldc, col0, lane);
 #pragma unroll
-  for (int g = 0; g < G; ++g)
+  for (int h = 0; h < BH / 16; ++h) {
+    if (slot < 0)
+      store_tile<VEC, G>(acc[h], C, (int64_t)src.window(t) * BH + 16 * h, M, ldc, col0, lane);
+    else
+      store_tile<VEC, G>(acc[h], partial, (int64_t)slot * BH + 16 * h, (int64_t)(slot + 1) * BH, ldc,
+                         col0, lane);
 #pragma unroll
-    for (int s = 0; s < VEC; ++s) acc[g][s] = f4{0.f, 0.f, 0.f, 0.f};
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int s = 0; s < VEC; ++s) acc[h][g][s] = f4{0.f, 0.f, 0.f, 0.f};
+  }
 }
 
 // One workgroup = WAVES waves on one (task group, column chunk); a column
@@ -215,16 +213,16 @@ __device__ __forceinline__ void flush_task(const Src& src, int t, f4 (&acc)[G][V
 // n_chunks, in group-major order (all chunks of a group adjacent) or
 // chunk-major order (one column chunk of every group first: the B rows a
 // chunk touches are narrower, so neighbouring windows' shared rows stay in
-// L2).  Each wave streams the group's blocks through one DEPTH-deep register
+// L2).  Each wave streams the group's units through one DEPTH-deep register
 // ring without draining it at task boundaries: the accumulator tile is
-// flushed and cleared when the block index crosses a task's end, so short
-// windows (banded matrices) keep the loads of the next windows in flight.
-// Every output element has exactly one writer per launch: no atomics.
-template <class Src, int VEC, int G, int WAVES, int DEPTH>
-__global__ __launch_bounds__(64 * WAVES) void spmm16x8_stream(
+// flushed and cleared when the unit index crosses a task's end.  Every
+// output element has exactly one writer per launch: no atomics.
+template <class Src, int BH, int BW, int VEC, int G, int WAVES, int DEPTH>
+__global__ __launch_bounds__(64 * WAVES) void spmm_stream(
     Src src, const float* __restrict__ B, float* __restrict__ C, float* __restrict__ partial,
     const int* __restrict__ sidx, const float* __restrict__ val, int M, int N, int64_t ldb,
     int64_t ldc, int n_chunks, int chunk_major) {
+  typedef Shape<BH, BW> S;
   constexpr int WCOLS = 16 * VEC * G;
   const int64_t nwg = (int64_t)gridDim.x;
   const int64_t lid = xcd_remap(blockIdx.x, nwg);
@@ -239,67 +237,75 @@ __global__ __launch_bounds__(64 * WAVES) void spmm16x8_stream(
   int t0, t1;
   src.group(grp, t0, t1);
   if (t0 >= t1) return;
-  f4 acc[G][VEC];
+  f4 acc[S::H][G][VEC];
 #pragma unroll
-  for (int g = 0; g < G; ++g)
+  for (int h = 0; h < S::H; ++h)
 #pragma unroll
-    for (int s = 0; s < VEC; ++s) acc[g][s] = f4{0.f, 0.f, 0.f, 0.f};
-  const int64_t bs = src.begin(t0), be = src.end(t1 - 1);
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int s = 0; s < VEC; ++s) acc[h][g][s] = f4{0.f, 0.f, 0.f, 0.f};
+  const int64_t us = src.begin(t0) * S::Q, ue = src.end(t1 - 1) * S::Q;
   int t = t0;
-  int64_t tend = src.end(t0);
-  if (bs < be) {
+  int64_t tend = src.end(t0) * S::Q;
+  if (us < ue) {
     const int k = lane >> 4;
     const int i = lane & 15;
-    const int a_off = swz16x8(8 * i + 2 * k);
-    Frag<VEC, G> f[DEPTH];
+    int a_off[S::Q][S::H];
+#pragma unroll
+    for (int q = 0; q < S::Q; ++q)
+#pragma unroll
+      for (int h = 0; h < S::H; ++h) a_off[q][h] = swizzle_2_2_3(BW * (16 * h + i) + 8 * q + 2 * k);
+    Frag<S::H, VEC, G> f[DEPTH];
     int2 idx[DEPTH];
-    const int64_t last = be - 1;
+    const int64_t last = ue - 1;
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
-      const int64_t blk = bs + d < last ? bs + d : last;
-      const int2 rows = *reinterpret_cast<const int2*>(sidx + blk * 8 + 2 * k);
-      load_frag<VEC, G>(f[d], B, val, blk, rows, a_off, ldb, col0);
-      const int64_t nblk = bs + DEPTH + d < last ? bs + DEPTH + d : last;
-      idx[d] = *reinterpret_cast<const int2*>(sidx + nblk * 8 + 2 * k);
+      const int64_t u = us + d < last ? us + d : last;
+      const int2 rows = *reinterpret_cast<const int2*>(sidx + u * 8 + 2 * k);
+      load_frag<BH, BW, VEC, G>(f[d], B, val, u, rows, a_off, ldb, col0);
+      const int64_t nu = us + DEPTH + d < last ? us + DEPTH + d : last;
+      idx[d] = *reinterpret_cast<const int2*>(sidx + nu * 8 + 2 * k);
     }
-    for (int64_t base = bs; base < be; base += DEPTH) {
+    for (int64_t base = us; base < ue; base += DEPTH) {
 #pragma unroll
       for (int d = 0; d < DEPTH; ++d) {
-        const int64_t blk = base + d;
-        if (blk < be) {
-          while (blk >= tend) {   // crossed into the next task (empty tasks flush zeros)
-            flush_task<Src, VEC, G>(src, t, acc, C, partial, M, ldc, col0, lane);
+        const int64_t u = base + d;
+        if (u < ue) {
+          while (u >= tend) {   // crossed into the next task (empty tasks flush zeros)
+            flush_task<Src, BH, VEC, G>(src, t, acc, C, partial, M, ldc, col0, lane);
             ++t;
-            tend = src.end(t);
+            tend = src.end(t) * S::Q;
           }
-          mma_frag<VEC, G>(f[d], acc);
+          mma_frag<S::H, VEC, G>(f[d], acc);
         }
-        const int64_t nblk = blk + DEPTH;
-        if (nblk < be) {
-          load_frag<VEC, G>(f[d], B, val, nblk, idx[d], a_off, ldb, col0);
-          const int64_t nn = nblk + DEPTH < last ? nblk + DEPTH : last;
+        const int64_t nu = u + DEPTH;
+        if (nu < ue) {
+          load_frag<BH, BW, VEC, G>(f[d], B, val, nu, idx[d], a_off, ldb, col0);
+          const int64_t nn = nu + DEPTH < last ? nu + DEPTH : last;
           idx[d] = *reinterpret_cast<const int2*>(sidx + nn * 8 + 2 * k);
         }
       }
     }
   }
-  for (; t < t1; ++t) flush_task<Src, VEC, G>(src, t, acc, C, partial, M, ldc, col0, lane);
+  for (; t < t1; ++t) flush_task<Src, BH, VEC, G>(src, t, acc, C, partial, M, ldc, col0, lane);
 }
 
 // out rows of window red_window[i] = sum over slots [red_slot_off[i],
-// red_slot_off[i+1]) of the partial tiles, in slot order (deterministic;
-// zero slots give zeros).  The atomic-free counterpart of the reference's
-// reduce_tcf_segments (examples/src_fp32/acc/testbed/custom_format_e2e.cu:
-// 832-853).  One thread per VEC consecutive columns.
+// red_slot_off[i+1]) of the partial tiles (tile_rows x N each), in slot
+// order (deterministic; zero slots give zeros).  The atomic-free
+// counterpart of the reference's reduce_tcf_segments
+// (examples/src_fp32/acc/testbed/custom_format_e2e.cu:832-853).  One thread
+// per VEC consecutive columns.
 template <int VEC>
 __global__ __launch_bounds__(256) void segment_reduce(const float* __restrict__ partial,
                                                       float* __restrict__ C,
                                                       const int* __restrict__ red_window,
                                                       const int* __restrict__ red_slot_off,
-                                                      int n_red, int M, int N, int64_t ldc) {
+                                                      int n_red, int tile_rows, int M, int N,
+                                                      int64_t ldc) {
   typedef typename VecT<VEC>::type V;
   const int64_t nv = N / VEC;
-  const int64_t per = 16 * nv;
+  const int64_t per = tile_rows * nv;
   const int64_t total = (int64_t)n_red * per;
   for (int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; id < total;
        id += (int64_t)gridDim.x * blockDim.x) {
@@ -307,17 +313,17 @@ __global__ __launch_bounds__(256) void segment_reduce(const float* __restrict__ 
     const int64_t within = id % per;
     const int r = (int)(within / nv);
     const int64_t cv = within % nv;
-    const int64_t row = (int64_t)red_window[i] * 16 + r;
+    const int64_t row = (int64_t)red_window[i] * tile_rows + r;
     if (row >= M) continue;
     V s;
     if constexpr (VEC == 1) s = 0.f; else { for (int q = 0; q < VEC; ++q) s[q] = 0.f; }
     for (int sl = red_slot_off[i]; sl < red_slot_off[i + 1]; ++sl)
-      s += *reinterpret_cast<const V*>(partial + ((int64_t)sl * 16 + r) * ldc + VEC * cv);
+      s += *reinterpret_cast<const V*>(partial + ((int64_t)sl * tile_rows + r) * ldc + VEC * cv);
     *reinterpret_cast<V*>(C + row * ldc + VEC * cv) = s;
   }
 }
 
-// CSR SpMM, one wave per row: lane owns VEC*NV consecutive columns per
+// CSR SpMM, one wave per row: lane owns VEC consecutive columns per
 // 64*VEC-column pass.  Edge-ordered fp32 accumulation, the arithmetic of the
 // reference's csr_spmm_value_kernel (examples/src_fp32/sr_bcrs/testbed/
 // SRBCRSSpMM_kernel.cu:66-87), laid out for wave64 vector loads.
@@ -368,7 +374,7 @@ static int pick_waves(int N, int wcols, int wg_cols) {
   return w >= 4 ? 4 : (w >= 2 ? 2 : 1);
 }
 
-template <class Src, int VEC, int G, int DEPTH>
+template <class Src, int BH, int BW, int VEC, int G, int DEPTH>
 static hipError_t launch_vg(const Src& src, int n_groups, const StreamArgs& a, const RunOpts& o,
                             hipStream_t st) {
   constexpr int WCOLS = 16 * VEC * G;
@@ -379,10 +385,10 @@ static hipError_t launch_vg(const Src& src, int n_groups, const StreamArgs& a, c
   if (nwg == 0) return hipSuccess;
   if (nwg > INT32_MAX) return hipErrorInvalidConfiguration;
   dim3 grid((unsigned)nwg);
-#define SRBCRS_LAUNCH(W)                                                                        \
-  hipLaunchKernelGGL((spmm16x8_stream<Src, VEC, G, W, DEPTH>), grid, dim3(64 * W), 0, st, src, \
-                     a.B, a.C, a.partial, a.sidx, a.val, a.M, a.N, a.ldb, a.ldc, n_chunks,      \
-                     o.chunk_major)
+#define SRBCRS_LAUNCH(W)                                                                       \
+  hipLaunchKernelGGL((spmm_stream<Src, BH, BW, VEC, G, W, DEPTH>), grid, dim3(64 * W), 0, st, \
+                     src, a.B, a.C, a.partial, a.sidx, a.val, a.M, a.N, a.ldb, a.ldc,          \
+                     n_chunks, o.chunk_major)
   switch (waves) {
     case 4: SRBCRS_LAUNCH(4); break;
     case 2: SRBCRS_LAUNCH(2); break;
@@ -392,30 +398,36 @@ static hipError_t launch_vg(const Src& src, int n_groups, const StreamArgs& a, c
   return hipGetLastError();
 }
 
+// vec (4, 2 or 1; 16*vec divides N) is chosen by the caller from N, the
+// leading dimensions and pointer alignment.  16x8: G = 2 column groups per
+// wave when the 128-column wave tile divides N and wider-than-64 workgroups
+// are allowed.  32x32 (four units and two row halves per block) keeps G = 1
+// to bound the register ring.
 template <class Src, int DEPTH>
 static hipError_t launch_d(const Src& src, int n_groups, const StreamArgs& a, int vec,
                            const RunOpts& o, hipStream_t st) {
+  if (a.blk_h == 32) {
+    if (vec == 4) return launch_vg<Src, 32, 32, 4, 1, DEPTH>(src, n_groups, a, o, st);
+    if (vec == 2) return launch_vg<Src, 32, 32, 2, 1, DEPTH>(src, n_groups, a, o, st);
+    return launch_vg<Src, 32, 32, 1, 1, DEPTH>(src, n_groups, a, o, st);
+  }
   if (vec == 4)
-    return (a.N % 128 == 0 && o.wg_cols != 64) ? launch_vg<Src, 4, 2, DEPTH>(src, n_groups, a, o, st)
-                                              : launch_vg<Src, 4, 1, DEPTH>(src, n_groups, a, o, st);
-  if (vec == 2) return launch_vg<Src, 2, 1, DEPTH>(src, n_groups, a, o, st);
-  return launch_vg<Src, 1, 1, DEPTH>(src, n_groups, a, o, st);
+    return (a.N % 128 == 0 && o.wg_cols != 64) ? launch_vg<Src, 16, 8, 4, 2, DEPTH>(src, n_groups, a, o, st)
+                                              : launch_vg<Src, 16, 8, 4, 1, DEPTH>(src, n_groups, a, o, st);
+  if (vec == 2) return launch_vg<Src, 16, 8, 2, 1, DEPTH>(src, n_groups, a, o, st);
+  return launch_vg<Src, 16, 8, 1, 1, DEPTH>(src, n_groups, a, o, st);
 }
 
 template <class Src>
 static hipError_t launch_src(const Src& src, int n_groups, const StreamArgs& a, int vec,
                              const RunOpts& o, hipStream_t st) {
   switch (o.depth) {
-    case 2: return launch_d<Src, 2>(src, n_groups, a, vec, o, st);
+    case 4: return launch_d<Src, 4>(src, n_groups, a, vec, o, st);
     case 8: return launch_d<Src, 8>(src, n_groups, a, vec, o, st);
-    default: return launch_d<Src, 4>(src, n_groups, a, vec, o, st);
+    default: return launch_d<Src, 2>(src, n_groups, a, vec, o, st);
   }
 }
 
-// vec (4, 2 or 1; 16*vec divides N) is chosen by the caller from N, the
-// leading dimensions and pointer alignment; G = 2 column groups per wave when
-// the 128-column wave tile divides N (and 64-column workgroups are not
-// requested); DEPTH = blocks in flight per wave.
 hipError_t launch_row(const StreamArgs& a, const int* soff, int Mo, int vec, const RunOpts& o,
                       hipStream_t st) {
   const int wpw = o.windows_per_wave > 0 ? o.windows_per_wave : 1;
@@ -431,18 +443,18 @@ hipError_t launch_tasks(const StreamArgs& a, const TaskTable& t, int vec, const 
 
 hipError_t launch_reduce(const ReduceArgs& a, int vec, hipStream_t st) {
   if (a.n_red == 0) return hipSuccess;
-  const int64_t total = (int64_t)a.n_red * 16 * (a.N / vec);
+  const int64_t total = (int64_t)a.n_red * a.tile_rows * (a.N / vec);
   int64_t blocks = (total + 255) / 256;
   if (blocks > 65536) blocks = 65536;
   if (vec == 4)
     hipLaunchKernelGGL(segment_reduce<4>, dim3((unsigned)blocks), dim3(256), 0, st, a.partial, a.C,
-                       a.red_window, a.red_slot_off, a.n_red, a.M, a.N, a.ldc);
+                       a.red_window, a.red_slot_off, a.n_red, a.tile_rows, a.M, a.N, a.ldc);
   else if (vec == 2)
     hipLaunchKernelGGL(segment_reduce<2>, dim3((unsigned)blocks), dim3(256), 0, st, a.partial, a.C,
-                       a.red_window, a.red_slot_off, a.n_red, a.M, a.N, a.ldc);
+                       a.red_window, a.red_slot_off, a.n_red, a.tile_rows, a.M, a.N, a.ldc);
   else
     hipLaunchKernelGGL(segment_reduce<1>, dim3((unsigned)blocks), dim3(256), 0, st, a.partial, a.C,
-                       a.red_window, a.red_slot_off, a.n_red, a.M, a.N, a.ldc);
+                       a.red_window, a.red_slot_off, a.n_red, a.tile_rows, a.M, a.N, a.ldc);
   return hipGetLastError();
 }
 

@@ -1,0 +1,140 @@
+"""GPU tests of the drop-in module surface (mask_amd.SRBCRSSpMM mirrors the
+reference's SRBCRSSpMM extension) and of the 32x32 base variant."""
+from __future__ import annotations
+
+import itertools
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+from tests.helpers import assert_gate, gate, random_csr
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(*a):
+    print("[case]", *a, flush=True)
+
+
+def _dev_csr(rowptr, colind, values):
+    import torch
+    return (torch.from_numpy(colind).cuda(), torch.from_numpy(rowptr).cuda(), torch.from_numpy(values).cuda())
+
+
+@pytest.mark.parametrize("blk", [(16, 8), (32, 32)])
+def test_preprocess_tuple_matches_oracle(gpu, blk):
+    import torch
+    from mask_amd import SRBCRSSpMM as S
+    bh, bw = blk
+    M, K = 203, 700
+    rowptr, colind, values = random_csr(M, K, 0.03, seed=5, unsorted=True, empty_rows=0.2)
+    _say("preprocess", blk, M, K)
+    ci, rp, vv = _dev_csr(rowptr, colind, values)
+    mo = (M + bh - 1) // bh
+    bp = torch.zeros(mo, dtype=torch.int32, device="cuda")
+    e2c = torch.zeros(colind.size, dtype=torch.int32, device="cuda")
+    e2r = torch.zeros(colind.size, dtype=torch.int32, device="cuda")
+    fn = S.preprocess_gpu_16x8 if blk == (16, 8) else S.preprocess_gpu
+    rwo, rowid, tile_id, toff, a2x, total = fn(ci, rp, vv, M, bh, bw, bp, e2c, e2r)
+    torch.cuda.synchronize()
+    o = oracle.convert(rowptr, colind, values, M, bh, bw)
+    assert total == o["total"]
+    assert np.array_equal(rwo.cpu().numpy(), o["soff"])
+    assert np.array_equal(tile_id.cpu().numpy(), o["sidx"])
+    assert np.array_equal(bp.cpu().numpy(), o["block_partition"])
+    assert np.array_equal(e2c.cpu().numpy(), o["edge_to_col"])
+    assert np.array_equal(e2r.cpu().numpy(), o["edge_to_row"])
+    assert rowid.numel() == total and int(rowid.abs().sum()) == 0
+    assert toff.numel() == 1 and a2x.numel() == 1
+    # the plan's device values are the oracle's swizzled blocks, bit for bit
+    val = S.plan_for(rwo).block_values()
+    assert val.cpu().numpy().tobytes() == o["val"].tobytes()
+
+
+@pytest.mark.parametrize("blk", [(16, 8), (32, 32)])
+@pytest.mark.parametrize("N", [16, 64, 96, 512])
+def test_run_matches_oracle(gpu, blk, N):
+    import torch
+    from mask_amd import SRBCRSSpMM as S
+    bh, bw = blk
+    M, K = 150, 400
+    rowptr, colind, values = random_csr(M, K, 0.05, seed=N, empty_rows=0.1)
+    B = np.random.default_rng(N).uniform(-1, 1, (K, N)).astype(np.float32)
+    _say("run", blk, M, K, N)
+    ci, rp, vv = _dev_csr(rowptr, colind, values)
+    z = torch.zeros(1, dtype=torch.int32, device="cuda")
+    pre = S.preprocess_gpu_16x8 if blk == (16, 8) else S.preprocess_gpu
+    run = S.run_SRBCRS_16x8 if blk == (16, 8) else S.run_SRBCRS
+    runb = S.run_SRBCRS_16x8_balance if blk == (16, 8) else S.run_SRBCRS_balance
+    rwo, _, tid, toff, a2x, _ = pre(ci, rp, vv, M, bh, bw, z, z, z)
+    dB = torch.from_numpy(B).cuda()
+    (out,) = run(dB, rwo, tid, toff, a2x, M, colind.size, "")
+    torch.cuda.synchronize()
+    assert out.shape == (M, N)
+    assert_gate(gate(out.cpu().numpy(), rowptr, colind, values, B, M))
+    (outb,) = runb(dB, rwo, tid, toff, a2x, M, "")
+    assert torch.equal(out, outb)
+    for plan_str in ("split:2", "strict_lb:3", "multi_bind"):
+        (o2,) = run(dB, rwo, tid, toff, a2x, M, colind.size, plan_str)
+        assert_gate(gate(o2.cpu().numpy(), rowptr, colind, values, B, M))
+
+
+def test_run_errors(gpu, monkeypatch):
+    import torch
+    from mask_amd import SRBCRSSpMM as S
+    M, K = 40, 50
+    rowptr, colind, values = random_csr(M, K, 0.1, seed=1)
+    ci, rp, vv = _dev_csr(rowptr, colind, values)
+    z = torch.zeros(1, dtype=torch.int32, device="cuda")
+    rwo, _, tid, toff, a2x, _ = S.preprocess_gpu_16x8(ci, rp, vv, M, 16, 8, z, z, z)
+    dB = torch.ones((K, 64), device="cuda")
+    with pytest.raises(RuntimeError, match="cache miss"):
+        S.run_SRBCRS_16x8(dB, rwo.clone(), tid, toff, a2x, M, 0, "")
+    with pytest.raises(RuntimeError, match="num_nodes mismatch"):
+        S.run_SRBCRS_16x8(dB, rwo, tid, toff, a2x, M + 1, 0, "")
+    with pytest.raises(RuntimeError, match="variant mismatch"):
+        S.run_SRBCRS(dB, rwo, tid, toff, a2x, M, 0, "")
+    with pytest.raises(RuntimeError, match="divisible by 16/32/64"):
+        S.run_SRBCRS_16x8(torch.ones((K, 40), device="cuda"), rwo, tid, toff, a2x, M, 0, "")
+    with pytest.raises(RuntimeError, match="blk_h mismatch"):
+        S.preprocess_gpu_16x8(ci, rp, vv, M, 32, 8, z, z, z)
+    with pytest.raises(RuntimeError, match="must be float32"):
+        S.run_SRBCRS_16x8(dB.double(), rwo, tid, toff, a2x, M, 0, "")
+    monkeypatch.setenv("SRBCRS_TILE_B", "7")
+    with pytest.raises(RuntimeError, match="Invalid SRBCRS_TILE_B"):
+        S.run_SRBCRS_16x8(dB, rwo, tid, toff, a2x, M, 0, "")
+    monkeypatch.delenv("SRBCRS_TILE_B")
+    (out,) = S.run_SRBCRS_16x8(torch.ones((K, 0), device="cuda"), rwo, tid, toff, a2x, M, 0, "")
+    assert out.shape == (M, 0)
+    # a matrix without blocks is refused like the reference (CSR fallback disabled)
+    e_rp = torch.zeros(M + 1, dtype=torch.int32, device="cuda")
+    e_ci = torch.zeros(0, dtype=torch.int32, device="cuda")
+    e_v = torch.zeros(0, dtype=torch.float32, device="cuda")
+    r2, _, t2, o2, x2, total = S.preprocess_gpu_16x8(e_ci, e_rp, e_v, M, 16, 8, z, z, z)
+    assert total == 0
+    with pytest.raises(RuntimeError, match="empty preprocessed blocks"):
+        S.run_SRBCRS_16x8(dB, r2, t2, o2, x2, M, 0, "")
+    # B with too few rows for the matrix's columns is refused before launch
+    from mask_amd._capi import SrbcrsError
+    with pytest.raises(SrbcrsError, match="references column"):
+        S.plan_for(rwo).run(torch.ones((int(colind.max()), 64), device="cuda"))
+
+
+def test_32x32_knobs_and_schedules(gpu):
+    import torch
+    from mask_amd.SRBCRSSpMM import Plan
+    M, K, N = 300, 2000, 128
+    rowptr, colind, values = random_csr(M, K, 0.02, seed=8, empty_rows=0.3, heavy_rows=4, heavy_len=900)
+    B = np.random.default_rng(8).uniform(-1, 1, (K, N)).astype(np.float32)
+    _say("32x32 knobs", M, K, N)
+    plan = Plan(*(torch.from_numpy(a).cuda() for a in (rowptr, colind, values)), M, 32, 32)
+    dB = torch.from_numpy(B).cuda()
+    ref = plan.run(dB).cpu().numpy()
+    assert_gate(gate(ref, rowptr, colind, values, B, M))
+    for depth, tile_b, wgc, go in itertools.product([2, 4, 8], [0, 16, 32], [0, 64], [1, 2]):
+        out = plan.run(dB, depth=depth, tile_b=tile_b, wg_cols=wgc, grid_order=go)
+        assert np.array_equal(out.cpu().numpy(), ref), (depth, tile_b, wgc, go)
+    for pol in (("split", 0), ("split", 2), ("strict_lb", 5), ("multi_bind", 0)):
+        plan.set_schedule(*pol)
+        assert_gate(gate(plan.run(dB).cpu().numpy(), rowptr, colind, values, B, M))
