@@ -198,3 +198,49 @@ def test_exeplan_schedule_parsing(monkeypatch):
     assert S._schedule_from_exeplan("strict_lb:32") == ("strict_lb", 32)
     monkeypatch.setenv("SPARSENE_SRBCRS_SCHEDULE", "split")
     assert S._schedule_from_exeplan("") == ("split", 0)
+
+
+# ---- GCN bridge host logic ------------------------------------------------------------
+
+def test_select_tile_b_and_padding(monkeypatch):
+    torch = pytest.importorskip("torch")
+    from mask_amd import external_backend_spmm as E
+    monkeypatch.delenv("SPARSENE_SRBCRS_TILE_B", raising=False)
+    # least padding, ties to the larger tile (external_backend_spmm.py:72-84)
+    assert E._select_tile_b(512, "SPARSENE_SRBCRS_TILE_B") == 64
+    assert E._select_tile_b(40, "SPARSENE_SRBCRS_TILE_B") == 16    # 48 vs 64
+    assert E._select_tile_b(96, "SPARSENE_SRBCRS_TILE_B") == 32
+    assert E._select_tile_b(100, "SPARSENE_SRBCRS_TILE_B") == 16   # 112 vs 128
+    monkeypatch.setenv("SPARSENE_SRBCRS_TILE_B", "64")
+    assert E._select_tile_b(40, "SPARSENE_SRBCRS_TILE_B") == 64
+    monkeypatch.setenv("SPARSENE_SRBCRS_TILE_B", "junk")
+    assert E._select_tile_b(40, "SPARSENE_SRBCRS_TILE_B") == 16
+    d = torch.arange(12, dtype=torch.float32).reshape(3, 4)
+    p, cols = E._pad_dense_to_tile(d, 16)
+    assert cols == 4 and p.shape == (3, 16) and torch.equal(p[:, :4], d) and not p[:, 4:].any()
+
+
+def test_variant_normalisation():
+    from mask_amd import external_backend_spmm as E
+    n = E.SRBCRSBackend._normalize_variant
+    assert n("") == "base" and n("SR_BCRS") == "base"
+    assert n("sr_bcrs_16x8") == "16x8"
+    assert n("multibind_16x8") == "16x8_multi_binding"
+    assert n("strict-lb") == "strict_lb"
+    assert E._VARIANT_PLAN["16x8_strict_lb"] == ((16, 8), ("strict_lb", 0))
+    assert E.SRBCRSBackend._variant_tile_shape("base") == (32, 32)
+
+
+def test_csr_transpose_matches_dense():
+    from mask_amd.gcn import csr_transpose
+    M, K = 50, 70
+    rowptr, colind, values = random_csr(M, K, 0.1, seed=2)
+    A = np.zeros((M, K), np.float32)
+    for r in range(M):
+        A[r, colind[rowptr[r]:rowptr[r + 1]]] = values[rowptr[r]:rowptr[r + 1]]
+    trp, tci, tv = csr_transpose(rowptr, colind, values, K)
+    At = np.zeros((K, M), np.float32)
+    for r in range(K):
+        assert (np.diff(tci[trp[r]:trp[r + 1]]) > 0).all()
+        At[r, tci[trp[r]:trp[r + 1]]] = tv[trp[r]:trp[r + 1]]
+    assert np.array_equal(At, A.T)
