@@ -165,7 +165,10 @@ def main():
                    "knobs": {"depth": args.depth or 2, "tile_b": args.tile_b, "wg_cols": args.wg_cols or 128,
                              "grid_order": args.grid_order or 1, "windows_per_wave": args.wpw or 1}},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(m.name, N, args.kernel,
+                                                 not (args.depth or args.tile_b or args.wg_cols or args.grid_order
+                                                      or args.wpw) and args.schedule == "auto"),
                      "algorithmic_bytes": int(ab), "compulsory_bytes": int(compulsory),
                      "compulsory_frac": round(compulsory / t_s / 1e9 / HBM_PEAK_GBS, 4),
                      "mfma_padded_tflops": round(padded_flops / t_s / 1e12, 3),
@@ -180,6 +183,22 @@ def main():
         result["cpu_baseline"] = cpu_baseline(m, B_host, N, args.cpu_seconds)
 
     print(json.dumps(result), flush=True)
+
+
+def measured_traffic(workload, N, kernel, default_knobs):
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 PMC summary (FETCH_SIZE and WRITE_SIZE runs, scaled by the
+    copy-kernel calibration), when one exists for this workload and the
+    default kernel configuration; None otherwise."""
+    if kernel != "srbcrs" or not default_knobs:
+        return None
+    path = ROOT / "profiles" / f"spmm_stream_{workload.replace('^', '')}_N{N}.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        if line.startswith("traffic_bytes:"):
+            return int(line.split(":", 1)[1])
+    return None
 
 
 def datasets_soff(plan):
