@@ -47,21 +47,40 @@ def _run(cmd):
 
 
 def build(verbose: bool = False) -> Path:
+    """Compile the library and the emitter's default operators (in parallel)."""
+    from concurrent.futures import ThreadPoolExecutor
     hipcc = _hipcc()
     objdir = PKG / "_build"
     objdir.mkdir(exist_ok=True)
-    objs = []
-    for src in ("srbcrs_kernels.hip", "srbcrs_capi.cpp"):
+
+    def compile_obj(src):
         obj = objdir / (src.rsplit(".", 1)[0] + ".o")
-        cmd = [hipcc, *DEVICE_FLAGS, f"-I{ROOT / 'include'}", "-x", "hip", "-c", str(CSRC / src), "-o", str(obj)]
-        out = _run(cmd)
+        out = _run([hipcc, *DEVICE_FLAGS, f"-I{ROOT / 'include'}", "-x", "hip", "-c", str(CSRC / src), "-o", str(obj)])
         if verbose and out:
             print(out)
-        objs.append(str(obj))
+        return str(obj)
+
+    with ThreadPoolExecutor(max_workers=4) as ex:
+        gen = [ex.submit(build_generated_one, bm, bk) for bm, bk in GENERATED_SHAPES]
+        objs = list(ex.map(compile_obj, ("srbcrs_kernels.hip", "srbcrs_capi.cpp")))
+        for f in gen:
+            f.result()
     tmp = LIB.with_suffix(".so.tmp")
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *objs, "-lpthread"])
     os.replace(tmp, LIB)
     return LIB
+
+
+GENERATED = PKG / "generated"
+GENERATED_SHAPES = ((16, 8), (32, 32))
+
+
+def build_generated_one(bm: int, bk: int) -> str:
+    """Emit and compile the default-strategy operator of the HIP emitter for
+    one SR-BCRS block shape into mask_amd/generated/."""
+    from .backend_registry import sr_bcrs_spec
+    from .emitter import lower_format_operator
+    return lower_format_operator(sr_bcrs_spec(bm, bk), GENERATED / f"sr_bcrs_{bm}x{bk}.so")["operator_path"]
 
 
 if __name__ == "__main__":

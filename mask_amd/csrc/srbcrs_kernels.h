@@ -5,7 +5,7 @@
 
 namespace srbcrs {
 
-constexpr int kNumXcd = 8;   // MI355X: 8 XCDs, 32 CUs each
+
 
 // Launch knobs (template / runtime parameters of the SR-BCRS kernels).
 struct RunOpts {

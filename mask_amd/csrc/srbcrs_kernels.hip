@@ -1,367 +1,11 @@
-// SR-BCRS fp32 SpMM kernels for gfx950 (CDNA4, wave64).
-//
-// C[M x N] = A[M x K] * B[K x N], A in SR-BCRS with BH x BW blocks
-// (16 x 8, or the 32 x 32 base variant):
-//   soff[Mo+1]      block offsets per BH-row window
-//   sidx[BW*nb]     the BW B-row (column) indices of each block
-//   val[BH*BW*nb]   the block values, BH x BW row-major with CuTe
-//                   Swizzle<2,2,3> applied to the offset:
-//                   pos(r,c) = o ^ ((o & 0x60) >> 3), o = BW*r + c.
-// This is the data the reference's sr_bcrs_spmm_kernel_tf32<16,64,8> (and
-// its 32x32 sibling) consumes (examples/src_fp32/sr_bcrs/testbed/
-// kernel.inc:1590-1700); the arithmetic here is native fp32 MFMA instead of
-// TF32 MMA.
-//
-// Units.  A block is BW/8 "units" of 8 columns; unit u of block b has
-// index b*(BW/8) + q and its 8 B-row indices are sidx[8u .. 8u+8), so the
-// kernel walks one contiguous unit sequence for either block shape.
-//
-// MFMA mapping.  v_mfma_f32_16x16x4_f32 (wave64) computes D(16x16) +=
-// A(16x4) * B(4x16) with lane l holding A[l%16][l/16], B[l/16][l%16] and
-// D[4*(l/16)+r][l%16], r = 0..3.  A unit times one 16-row half of the
-// block is two such k-steps; the unit's 8 columns split as k-step 0 =
-// {0,2,4,6}, k-step 1 = {1,3,5,7}, so lane (i = l%16, k = l/16) needs
-// A[i][8q+2k] and A[i][8q+2k+1].  The swizzle only touches offset bits 2..3,
-// so those two values sit next to each other in memory: one 8-byte load per
-// lane and row half fetches the lane's A fragment.
-//
-// Column mapping.  A wave owns 16*VEC*G output columns.  In column group g
-// lane j = l%16 owns columns base + 16*VEC*g + VEC*j + s (s < VEC): one
-// VEC-wide vector load per (B row, g) per lane, VEC MFMAs per k-step, g and
-// row half.  For VEC = 4 a wave's B load covers four 256-byte row segments.
-//
-// No LDS: every B element is used by exactly one wave (waves split N), so
-// staging through LDS adds no reuse; latency is hidden by a register ring
-// DEPTH units deep, with the B-row indices fetched one ring further ahead.
+// Host launchers of the SR-BCRS kernels (templates in srbcrs_stream.hpp).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
 #include "srbcrs_kernels.h"
+#include "srbcrs_stream.hpp"
 
 namespace srbcrs {
-
-typedef float f4 __attribute__((ext_vector_type(4)));
-typedef float f2 __attribute__((ext_vector_type(2)));
-
-template <int VEC> struct VecT;
-template <> struct VecT<1> { typedef float type; };
-template <> struct VecT<2> { typedef f2 type; };
-template <> struct VecT<4> { typedef f4 type; };
-
-template <int VEC>
-__device__ __forceinline__ float vget(const typename VecT<VEC>::type& v, int s);
-template <> __device__ __forceinline__ float vget<1>(const float& v, int) { return v; }
-template <> __device__ __forceinline__ float vget<2>(const f2& v, int s) { return v[s]; }
-template <> __device__ __forceinline__ float vget<4>(const f4& v, int s) { return v[s]; }
-
-__device__ __forceinline__ int swizzle_2_2_3(int o) { return o ^ ((o & 0x60) >> 3); }
-
-// Map the hardware workgroup id to a logical one so that each XCD (the
-// dispatcher deals workgroups round-robin over the 8 XCDs) receives a
-// contiguous range of logical ids: neighbouring row windows, which share B
-// rows in banded matrices, then share one L2.
-__device__ __forceinline__ int64_t xcd_remap(int64_t id, int64_t n) {
-  const int64_t q = n / kNumXcd, r = n % kNumXcd;
-  const int64_t x = id % kNumXcd, t = id / kNumXcd;
-  return x * q + (x < r ? x : r) + t;
-}
-
-// Block geometry: BH x BW blocks, H = BH/16 row halves, Q = BW/8 units.
-template <int BH, int BW>
-struct Shape {
-  static constexpr int H = BH / 16;
-  static constexpr int Q = BW / 8;
-  static constexpr int SIZE = BH * BW;
-};
-
-// One unit in flight: the lane's A fragments (one per row half) and its B
-// vectors for the two k-steps.
-template <int H, int VEC, int G>
-struct Frag {
-  typedef typename VecT<VEC>::type V;
-  f2 a[H];       // A[16h+i][8q+2k], A[16h+i][8q+2k+1]
-  V b0[G];       // B[sidx[8u+2k]][cols of g]
-  V b1[G];       // B[sidx[8u+2k+1]][cols of g]
-};
-
-template <int BH, int BW, int VEC, int G>
-__device__ __forceinline__ void load_frag(Frag<BH / 16, VEC, G>& f, const float* __restrict__ B,
-                                          const float* __restrict__ val, int64_t unit, int2 rows,
-                                          const int (&a_off)[BW / 8][BH / 16], int64_t ldb,
-                                          int col0) {
-  typedef Shape<BH, BW> S;
-  typedef typename VecT<VEC>::type V;
-  const int64_t blk = unit / S::Q;
-  const int q = (int)(unit % S::Q);
-  const float* vb = val + blk * S::SIZE;
-#pragma unroll
-  for (int h = 0; h < S::H; ++h) {
-    int off = a_off[0][h];
-#pragma unroll
-    for (int qq = 1; qq < S::Q; ++qq)
-      if (q == qq) off = a_off[qq][h];
-    f.a[h] = *reinterpret_cast<const f2*>(vb + off);
-  }
-  const float* r0 = B + (int64_t)rows.x * ldb + col0;
-  const float* r1 = B + (int64_t)rows.y * ldb + col0;
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    f.b0[g] = *reinterpret_cast<const V*>(r0 + 16 * VEC * g);
-    f.b1[g] = *reinterpret_cast<const V*>(r1 + 16 * VEC * g);
-  }
-}
-
-template <int H, int VEC, int G>
-__device__ __forceinline__ void mma_frag(const Frag<H, VEC, G>& f, f4 (&acc)[H][G][VEC]) {
-#pragma unroll
-  for (int h = 0; h < H; ++h)
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int s = 0; s < VEC; ++s) {
-        acc[h][g][s] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[h].x, vget<VEC>(f.b0[g], s), acc[h][g][s], 0, 0, 0);
-        acc[h][g][s] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[h].y, vget<VEC>(f.b1[g], s), acc[h][g][s], 0, 0, 0);
-      }
-}
-
-// Store a 16 x (16*VEC*G) accumulator tile.  row0 is the tile's first row in
-// `out`, rows >= row_limit are skipped (M % 16 != 0).
-template <int VEC, int G>
-__device__ __forceinline__ void store_tile(const f4 (&acc)[G][VEC], float* __restrict__ out,
-                                           int64_t row0, int64_t row_limit, int64_t ldc, int col0,
-                                           int lane) {
-  typedef typename VecT<VEC>::type V;
-  const int k = lane >> 4;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int64_t row = row0 + 4 * k + r;
-    if (row < row_limit) {
-      float* p = out + row * ldc + col0;
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        V v;
-        if constexpr (VEC == 1) {
-          v = acc[g][0][r];
-        } else {
-#pragma unroll
-          for (int s = 0; s < VEC; ++s) v[s] = acc[g][s][r];
-        }
-        __builtin_nontemporal_store(v, reinterpret_cast<V*>(p + 16 * VEC * g));
-      }
-    }
-  }
-}
-
-// Task sources.  A task is a block range [begin, end) of one row window
-// whose BH-row result goes straight into C (slot < 0) or into partial slot
-// `slot` for the segment reduction.  A group is a run of consecutive tasks
-// with contiguous block ranges, processed by one wave per column chunk.
-
-// Row schedule: task t = row window t, groups of `wpw` consecutive windows.
-struct RowTasks {
-  const int* __restrict__ soff;
-  int Mo;
-  int wpw;
-  __device__ __forceinline__ void group(int g, int& t0, int& t1) const {
-    t0 = g * wpw;
-    t1 = t0 + wpw < Mo ? t0 + wpw : Mo;
-  }
-  __device__ __forceinline__ int64_t begin(int t) const { return soff[t]; }
-  __device__ __forceinline__ int64_t end(int t) const { return soff[t + 1]; }
-  __device__ __forceinline__ int window(int t) const { return t; }
-  __device__ __forceinline__ int slot(int) const { return -1; }
-};
-
-// Table schedule (split / strict_lb / multi_bind) built on the host.
-struct TableTasks {
-  const int* __restrict__ group_off;
-  const int* __restrict__ task_begin;
-  const int* __restrict__ task_end;
-  const int* __restrict__ task_window;
-  const int* __restrict__ task_slot;
-  __device__ __forceinline__ void group(int g, int& t0, int& t1) const {
-    t0 = group_off[g];
-    t1 = group_off[g + 1];
-  }
-  __device__ __forceinline__ int64_t begin(int t) const { return task_begin[t]; }
-  __device__ __forceinline__ int64_t end(int t) const { return task_end[t]; }
-  __device__ __forceinline__ int window(int t) const { return task_window[t]; }
-  __device__ __forceinline__ int slot(int t) const { return task_slot[t]; }
-};
-
-template <class Src, int BH, int VEC, int G>
-__device__ __forceinline__ void flush_task(const Src& src, int t, f4 (&acc)[BH / 16][G][VEC],
-                                           float* __restrict__ C, float* __restrict__ partial,
-                                           int M, int64_t ldc, int col0, int lane) {
-  const int slot = src.slot(t);
-#pragma unroll
-  for (int h = 0; h < BH / 16; ++h) {
-    if (slot < 0)
-      store_tile<VEC, G>(acc[h], C, (int64_t)src.window(t) * BH + 16 * h, M, ldc, col0, lane);
-    else
-      store_tile<VEC, G>(acc[h], partial, (int64_t)slot * BH + 16 * h, (int64_t)(slot + 1) * BH, ldc,
-                         col0, lane);
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int s = 0; s < VEC; ++s) acc[h][g][s] = f4{0.f, 0.f, 0.f, 0.f};
-  }
-}
-
-// One workgroup = WAVES waves on one (task group, column chunk); a column
-// chunk is WAVES * 16*VEC*G columns.  The grid is 1-D over n_groups *
-// n_chunks, in group-major order (all chunks of a group adjacent) or
-// chunk-major order (one column chunk of every group first: the B rows a
-// chunk touches are narrower, so neighbouring windows' shared rows stay in
-// L2).  Each wave streams the group's units through one DEPTH-deep register
-// ring without draining it at task boundaries: the accumulator tile is
-// flushed and cleared when the unit index crosses a task's end.  Every
-// output element has exactly one writer per launch: no atomics.
-template <class Src, int BH, int BW, int VEC, int G, int WAVES, int DEPTH>
-__global__ __launch_bounds__(64 * WAVES) void spmm_stream(
-    Src src, const float* __restrict__ B, float* __restrict__ C, float* __restrict__ partial,
-    const int* __restrict__ sidx, const float* __restrict__ val, int M, int N, int64_t ldb,
-    int64_t ldc, int n_chunks, int chunk_major) {
-  typedef Shape<BH, BW> S;
-  constexpr int WCOLS = 16 * VEC * G;
-  const int64_t nwg = (int64_t)gridDim.x;
-  const int64_t lid = xcd_remap(blockIdx.x, nwg);
-  const int64_t n_units = nwg / n_chunks;
-  const int grp = (int)(chunk_major ? lid % n_units : lid / n_chunks);
-  const int chunk = (int)(chunk_major ? lid / n_units : lid % n_chunks);
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
-  const int wcol = (chunk * WAVES + wave) * WCOLS;
-  if (wcol >= N) return;
-  const int col0 = wcol + VEC * (lane & 15);
-  int t0, t1;
-  src.group(grp, t0, t1);
-  if (t0 >= t1) return;
-  f4 acc[S::H][G][VEC];
-#pragma unroll
-  for (int h = 0; h < S::H; ++h)
-#pragma unroll
-    for (int g = 0; g < G; ++g)
-#pragma unroll
-      for (int s = 0; s < VEC; ++s) acc[h][g][s] = f4{0.f, 0.f, 0.f, 0.f};
-  const int64_t us = src.begin(t0) * S::Q, ue = src.end(t1 - 1) * S::Q;
-  int t = t0;
-  int64_t tend = src.end(t0) * S::Q;
-  if (us < ue) {
-    const int k = lane >> 4;
-    const int i = lane & 15;
-    int a_off[S::Q][S::H];
-#pragma unroll
-    for (int q = 0; q < S::Q; ++q)
-#pragma unroll
-      for (int h = 0; h < S::H; ++h) a_off[q][h] = swizzle_2_2_3(BW * (16 * h + i) + 8 * q + 2 * k);
-    Frag<S::H, VEC, G> f[DEPTH];
-    int2 idx[DEPTH];
-    const int64_t last = ue - 1;
-#pragma unroll
-    for (int d = 0; d < DEPTH; ++d) {
-      const int64_t u = us + d < last ? us + d : last;
-      const int2 rows = *reinterpret_cast<const int2*>(sidx + u * 8 + 2 * k);
-      load_frag<BH, BW, VEC, G>(f[d], B, val, u, rows, a_off, ldb, col0);
-      const int64_t nu = us + DEPTH + d < last ? us + DEPTH + d : last;
-      idx[d] = *reinterpret_cast<const int2*>(sidx + nu * 8 + 2 * k);
-    }
-    for (int64_t base = us; base < ue; base += DEPTH) {
-#pragma unroll
-      for (int d = 0; d < DEPTH; ++d) {
-        const int64_t u = base + d;
-        if (u < ue) {
-          while (u >= tend) {   // crossed into the next task (empty tasks flush zeros)
-            flush_task<Src, BH, VEC, G>(src, t, acc, C, partial, M, ldc, col0, lane);
-            ++t;
-            tend = src.end(t) * S::Q;
-          }
-          mma_frag<S::H, VEC, G>(f[d], acc);
-        }
-        const int64_t nu = u + DEPTH;
-        if (nu < ue) {
-          load_frag<BH, BW, VEC, G>(f[d], B, val, nu, idx[d], a_off, ldb, col0);
-          const int64_t nn = nu + DEPTH < last ? nu + DEPTH : last;
-          idx[d] = *reinterpret_cast<const int2*>(sidx + nn * 8 + 2 * k);
-        }
-      }
-    }
-  }
-  for (; t < t1; ++t) flush_task<Src, BH, VEC, G>(src, t, acc, C, partial, M, ldc, col0, lane);
-}
-
-// out rows of window red_window[i] = sum over slots [red_slot_off[i],
-// red_slot_off[i+1]) of the partial tiles (tile_rows x N each), in slot
-// order (deterministic; zero slots give zeros).  The atomic-free
-// counterpart of the reference's reduce_tcf_segments
-// (examples/src_fp32/acc/testbed/custom_format_e2e.cu:832-853).  One thread
-// per VEC consecutive columns.
-template <int VEC>
-__global__ __launch_bounds__(256) void segment_reduce(const float* __restrict__ partial,
-                                                      float* __restrict__ C,
-                                                      const int* __restrict__ red_window,
-                                                      const int* __restrict__ red_slot_off,
-                                                      int n_red, int tile_rows, int M, int N,
-                                                      int64_t ldc) {
-  typedef typename VecT<VEC>::type V;
-  const int64_t nv = N / VEC;
-  const int64_t per = tile_rows * nv;
-  const int64_t total = (int64_t)n_red * per;
-  for (int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; id < total;
-       id += (int64_t)gridDim.x * blockDim.x) {
-    const int i = (int)(id / per);
-    const int64_t within = id % per;
-    const int r = (int)(within / nv);
-    const int64_t cv = within % nv;
-    const int64_t row = (int64_t)red_window[i] * tile_rows + r;
-    if (row >= M) continue;
-    V s;
-    if constexpr (VEC == 1) s = 0.f; else { for (int q = 0; q < VEC; ++q) s[q] = 0.f; }
-    for (int sl = red_slot_off[i]; sl < red_slot_off[i + 1]; ++sl)
-      s += *reinterpret_cast<const V*>(partial + ((int64_t)sl * tile_rows + r) * ldc + VEC * cv);
-    *reinterpret_cast<V*>(C + row * ldc + VEC * cv) = s;
-  }
-}
-
-// CSR SpMM, one wave per row: lane owns VEC consecutive columns per
-// 64*VEC-column pass.  Edge-ordered fp32 accumulation, the arithmetic of the
-// reference's csr_spmm_value_kernel (examples/src_fp32/sr_bcrs/testbed/
-// SRBCRSSpMM_kernel.cu:66-87), laid out for wave64 vector loads.
-template <int VEC, int UNROLL>
-__global__ __launch_bounds__(256) void csr_spmm_rowwave(
-    const int* __restrict__ rowptr, const int* __restrict__ colind,
-    const float* __restrict__ values, const float* __restrict__ B, float* __restrict__ C, int M,
-    int N, int64_t ldb, int64_t ldc) {
-  typedef typename VecT<VEC>::type V;
-  const int64_t nwg = (int64_t)gridDim.x;
-  const int64_t lid = xcd_remap(blockIdx.x, nwg);
-  const int64_t row = lid * 4 + (threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
-  if (row >= M) return;
-  const int e0 = rowptr[row], e1 = rowptr[row + 1];
-  for (int c = VEC * lane; c < N; c += 64 * VEC) {
-    V acc;
-    if constexpr (VEC == 1) acc = 0.f; else { for (int s = 0; s < VEC; ++s) acc[s] = 0.f; }
-    int e = e0;
-    for (; e + UNROLL <= e1; e += UNROLL) {
-      V bv[UNROLL];
-      float av[UNROLL];
-#pragma unroll
-      for (int u = 0; u < UNROLL; ++u) {
-        const int col = colind[e + u];
-        av[u] = values[e + u];
-        bv[u] = *reinterpret_cast<const V*>(B + (int64_t)col * ldb + c);
-      }
-#pragma unroll
-      for (int u = 0; u < UNROLL; ++u) acc += av[u] * bv[u];
-    }
-    for (; e < e1; ++e) {
-      const int col = colind[e];
-      acc += values[e] * *reinterpret_cast<const V*>(B + (int64_t)col * ldb + c);
-    }
-    *reinterpret_cast<V*>(C + row * ldc + c) = acc;
-  }
-}
 
 // ---------------------------------------------------------------------------
 // Host launchers.

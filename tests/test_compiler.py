@@ -1,0 +1,126 @@
+"""Compiler-side boundary (no GPU): select_backend for gfx950 and the HIP
+emitter's structure, knob mapping and determinism."""
+from __future__ import annotations
+
+import copy
+import json
+from types import SimpleNamespace
+
+import pytest
+
+from mask_amd.backend_registry import BackendPlan, select_backend, sr_bcrs_spec
+from mask_amd.emitter import HipCodeGenerator, KernelParams, emit_source, operator_sha256, params_from_strategy
+
+
+def test_select_backend_sr_bcrs():
+    p = select_backend(sr_bcrs_spec(), target="gfx950")
+    assert isinstance(p, BackendPlan)
+    assert (p.codegen_format_name, p.packing_mode, p.target) == ("SR_BCRS", "column_condensed_dense", "gfx950")
+    assert (p.physical_blk_m, p.physical_blk_k) == (16, 8)
+    assert (p.mma_m, p.mma_n, p.mma_k) == (16, 16, 4)
+    assert select_backend(sr_bcrs_spec(32, 32), target="MI355X").physical_blk_m == 32
+    # the inner condensed-block axis may be a variable-length sequence (dv)
+    spec = sr_bcrs_spec()
+    spec["levels"][1]["axes"][0]["type"] = "dv"
+    assert select_backend(spec).codegen_format_name == "SR_BCRS"
+
+
+@pytest.mark.parametrize("mutate,msg", [
+    (lambda s: s.update(atomic={"type": "mco", "x_axis": "X_i", "y_axis": "Y_si"}), "dense atomic"),
+    (lambda s: s["levels"].pop(), "two-level"),
+    (lambda s: s["levels"][0]["axes"][1].update(type="df"), "axis Y_s"),
+    (lambda s: s["atomic"].update(y_axis="Y_so"), "x_axis=X_i and y_axis=Y_si"),
+    (lambda s: s["atomic"].update(layout="col_major"), "row-major"),
+    (lambda s: s["params"].update(BLK_M=8), "BLK_M x BLK_K"),
+    (lambda s: s["params"].pop("BLK_K"), "concrete integer"),
+    (lambda s: s["levels"][0]["axes"][0].update(reorder="row_rcm"), "reorders"),
+])
+def test_select_backend_rejects(mutate, msg):
+    spec = copy.deepcopy(sr_bcrs_spec())
+    mutate(spec)
+    with pytest.raises(ValueError, match=msg):
+        select_backend(spec)
+
+
+def test_select_backend_targets_and_tiles():
+    with pytest.raises(ValueError, match="Unknown target"):
+        select_backend(sr_bcrs_spec(), target="sm80")
+    with pytest.raises(ValueError, match="tile_n"):
+        select_backend(sr_bcrs_spec(), tile_n=24)
+
+
+def _strategy(**kw):
+    tp = SimpleNamespace(tile_b=kw.get("tile_b", 64), b_smem_swizzle="swizzle_323",
+                         materialize_b_array_ref_to_smem=True)
+    pl = SimpleNamespace(enable_async_pipeline=kw.get("pipe", True), max_wait_prior=kw.get("mwp"),
+                         stage_shifts=kw.get("shifts", []))
+    rs = SimpleNamespace(execution_policy=kw.get("policy", "auto"), task_group_tiles=kw.get("tgt", 64),
+                         runtime_max_tiles_per_segment=kw.get("cap", 0))
+    return SimpleNamespace(tensor_placement=tp, pipeline=pl, runtime_schedule=rs)
+
+
+def test_strategy_knob_mapping():
+    plan = select_backend(sr_bcrs_spec())
+    p = params_from_strategy(None, plan)
+    assert p == KernelParams()
+    assert params_from_strategy(_strategy(tile_b=32), plan).vec == 2
+    assert params_from_strategy(_strategy(tile_b=32), plan).col_groups == 1
+    assert params_from_strategy(_strategy(mwp=3), plan).depth == 8
+    assert params_from_strategy(_strategy(shifts=[2, 1]), plan).depth == 4
+    assert params_from_strategy(_strategy(mwp=3, pipe=False), plan).depth == 2
+    sl = params_from_strategy(_strategy(policy="strict_lb", tgt=32), plan)
+    assert (sl.schedule, sl.schedule_param) == ("strict_lb", 32)
+    sp = params_from_strategy(_strategy(cap=48), plan)
+    assert (sp.schedule, sp.schedule_param) == ("split", 48)
+    # dict form of the strategy works too
+    assert params_from_strategy({"tensor_placement": {"tile_b": 16}}, plan).vec == 1
+    p32 = params_from_strategy(None, select_backend(sr_bcrs_spec(32, 32)))
+    assert (p32.blk_m, p32.blk_k, p32.col_groups) == (32, 32, 1)
+
+
+def test_emitted_source_structure_and_determinism():
+    plan = select_backend(sr_bcrs_spec())
+    prog = SimpleNamespace(name="SR_BCRS_16x8", attrs={
+        "format_name": "SR_BCRS", "strategy_decision": _strategy(tile_b=64, mwp=2),
+        "specialized_parameters": {"NNZ_HINT": 7}, "launch_contract": {"synchronization": "warp"}})
+    gen = HipCodeGenerator(plan)
+    src = gen.dump_nvop_program(prog)
+    assert src == gen.dump_nvop_program(prog)
+    for needle in ("#define SPARSENE_GENERATED_TILE_B 64", "#define SPARSENE_GENERATED_SUPPORTS_TASK_MAPPING 1",
+                   "#define SPARSENE_GENERATED_WAVE_SIZE 64", "#define SPARSENE_GENERATED_PIPELINE_DEPTH 4",
+                   "constexpr int NNZ_HINT = 7;", '#include "srbcrs_stream.hpp"',
+                   "srbcrs::spmm_stream<Src, kBH, kBW, kVEC, kG, kWAVES, kDEPTH>",
+                   'extern "C" int sparsene_generated_run(', 'extern "C" int sparsene_generated_run_tasks(',
+                   'extern "C" int sparsene_generated_reduce('):
+        assert needle in src, needle
+    meta = json.loads(src.split('R"JSON(')[1].split(')JSON"')[0])
+    assert meta["kernel_params"]["depth"] == 4 and meta["format_name"] == "SR_BCRS"
+    assert meta["notes"]["ignored_knobs"]["b_smem_swizzle"] == "swizzle_323"
+    assert "cp.async" not in src and "__syncwarp" not in src and "mma.sync" not in src
+    assert operator_sha256(src) != operator_sha256(emit_source(KernelParams()))
+
+
+def test_emitter_rejects_other_formats_and_bad_params():
+    gen = HipCodeGenerator()
+    with pytest.raises(NotImplementedError):
+        gen.dump_nvop_program(SimpleNamespace(name="x", attrs={"format_name": "ME_TCF"}))
+    with pytest.raises(ValueError, match="specialized"):
+        gen.dump_nvop_program(SimpleNamespace(name="x", attrs={"format_name": "SR_BCRS",
+                                                               "specialized_parameters": {"BLK_M": 4}}))
+    with pytest.raises(ValueError):
+        emit_source(KernelParams(depth=3))
+    with pytest.raises(ValueError):
+        emit_source(KernelParams(blk_m=32, blk_k=32, col_groups=2))
+
+
+def test_generated_operators_are_built():
+    """build() emitted and compiled both default operators (travel with the tree)."""
+    from mask_amd.build import GENERATED, GENERATED_SHAPES
+    for bm, bk in GENERATED_SHAPES:
+        so = GENERATED / f"sr_bcrs_{bm}x{bk}.so"
+        assert so.exists(), so
+        import ctypes
+        L = ctypes.CDLL(str(so))
+        L.sparsene_generated_metadata.restype = ctypes.c_char_p
+        meta = json.loads(L.sparsene_generated_metadata().decode())
+        assert meta["kernel_params"]["blk_m"] == bm and meta["target"] == "gfx950"
