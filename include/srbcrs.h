@@ -75,6 +75,10 @@ typedef struct srbcrs_plan_desc {
   const int32_t *d_soff;  /* row_window_offset, Mo + 1 */
   const int32_t *d_sidx;  /* tcblocktile_id, blk_w * total_blocks */
   const float *d_val;     /* swizzled block values, blk_h * blk_w * total_blocks */
+  int64_t packed_rows;    /* rows in the packed order (num_nodes unless sparse rows) */
+  const int32_t *d_row_map; /* packed row -> output row, NULL for the identity order */
+  int32_t packing;        /* SRBCRS_PACK_* */
+  int32_t dup_policy;     /* SRBCRS_DUP_* */
 } srbcrs_plan_desc;
 int srbcrs_plan_get(const srbcrs_plan *plan, srbcrs_plan_desc *out);
 
@@ -99,6 +103,59 @@ int srbcrs_plan_export_index(const srbcrs_plan *plan, int32_t *d_row_window_offs
  * device buffer.  A short buffer is an error. */
 int srbcrs_plan_export_values(const srbcrs_plan *plan, float *d_val, int64_t val_len,
                               void *stream);
+
+/* ---- Generated-operator packings (the reference's custom-format bridge,
+ * CFE:157-349 row reorders, CFE:483-488 sparse rows, CFE:496-640 packing,
+ * CFE:1083-1100 inverse output map).  A packed plan stores its rows in a
+ * new order (new row p <- original row order[p]); runs write each packed
+ * row straight to its original output row (the inverse map is fused into
+ * the kernel's store) and zero the rows the order leaves out. */
+#define SRBCRS_ORDER_IDENTITY 0
+#define SRBCRS_ORDER_RCM 1          /* reverse Cuthill-McKee (square matrices) */
+#define SRBCRS_ORDER_FIRST_COL 2    /* by first structural column */
+#define SRBCRS_ORDER_JACCARD 3      /* minhash buckets of 64, greedy Jaccard */
+#define SRBCRS_ORDER_SPARSE_ROWS 4  /* non-empty rows only */
+#define SRBCRS_ORDER_EXPLICIT 5     /* caller's order (distinct rows) */
+#define SRBCRS_PACK_CONDENSED 0     /* column-condensed dense tiles (SR-BCRS) */
+#define SRBCRS_PACK_FIXED_BLOCKS 1  /* active BW-aligned column blocks, dense */
+#define SRBCRS_DUP_LAST 0           /* duplicate (row, col): last value wins (preprocess_gpu) */
+#define SRBCRS_DUP_SUM 1            /* duplicates summed in edge order (CFE packing) */
+
+typedef struct srbcrs_pack_opts {
+  int32_t blk_h, blk_w;     /* (16, 8) or (32, 32) */
+  int32_t packing;          /* SRBCRS_PACK_* */
+  int32_t dup_policy;       /* SRBCRS_DUP_* */
+  int32_t row_order;        /* SRBCRS_ORDER_* */
+  const int32_t *order;     /* host, SRBCRS_ORDER_EXPLICIT only */
+  int32_t order_len;
+  int32_t K;                /* column count; required (> 0) for fixed blocks, -1 = unchecked */
+} srbcrs_pack_opts;
+
+/* Row order of a CSR matrix by `method` (SRBCRS_ORDER_RCM .. SPARSE_ROWS,
+ * or IDENTITY).  order has num_nodes entries; *order_len receives the
+ * number used (fewer than num_nodes only for SPARSE_ROWS). */
+int srbcrs_row_order(const int32_t *rowptr, const int32_t *colind, int32_t num_nodes, int64_t nnz,
+                     int32_t K, int32_t method, int32_t *order, int32_t *order_len);
+
+/* Host packing with explicit options (opts->row_order IDENTITY or
+ * EXPLICIT; resolve the other orders with srbcrs_row_order first).  soff
+ * has ceil(rows / blk_h) + 1 entries, rows = order_len or num_nodes. */
+int srbcrs_pack_count(const int32_t *rowptr, const int32_t *colind, int32_t num_nodes, int64_t nnz,
+                      const srbcrs_pack_opts *opts, int32_t *soff, int64_t *total_tiles);
+int srbcrs_pack_fill(const int32_t *rowptr, const int32_t *colind, const float *values,
+                     int32_t num_nodes, int64_t nnz, const srbcrs_pack_opts *opts,
+                     const int32_t *soff, int32_t *sidx, float *val);
+
+/* srbcrs_plan_create with packing options (NULL = the canonical 16x8
+ * preprocess_gpu conversion).  Edge maps (srbcrs_plan_write_edges) exist
+ * only for canonical plans. */
+int srbcrs_plan_create_ex(const int32_t *rowptr, const int32_t *colind, const float *values,
+                          int32_t num_nodes, int64_t nnz, const srbcrs_pack_opts *opts,
+                          int32_t is_device, void *stream, srbcrs_plan **out);
+
+/* The plan's row order (new -> original).  order needs room for
+ * num_nodes entries; *len receives the packed row count. */
+int srbcrs_plan_row_order(const srbcrs_plan *plan, int32_t *order, int32_t capacity, int32_t *len);
 
 /* ---- Execution schedules (host logic).  policy:
  *   "row"        one task per row window, written straight into C

@@ -42,7 +42,16 @@ class Plan:
     """A device-resident SR-BCRS matrix (owns a ``srbcrs_plan``)."""
 
     def __init__(self, rowptr, colind, values, num_nodes: int, blk_h: int = 16, blk_w: int = 8,
-                 device: Optional[torch.device] = None):
+                 device: Optional[torch.device] = None, packing: str = "column_condensed_dense",
+                 dup: str = "last", row_order="identity", K: Optional[int] = None):
+        """CSR (device tensors, or host arrays) -> device-resident plan.
+
+        The defaults are the reference's preprocess_gpu conversion.  The
+        generated-operator packings take ``packing`` ("column_condensed_dense"
+        / "active_fixed_blocks_dense"), ``dup`` ("last" / "sum"),
+        ``row_order`` ("identity", "row_rcm", "first_col_sort",
+        "jaccard_greedy", "sparse_rows", or an explicit new -> original
+        sequence) and the column count ``K`` (required for fixed blocks)."""
         L = _capi.lib()
         on_dev = isinstance(rowptr, Tensor) and rowptr.is_cuda
         if on_dev:
@@ -54,11 +63,21 @@ class Plan:
         self._keep = (rowptr, colind, values)
         nnz = int(colind.numel() if isinstance(colind, Tensor) else len(colind))
         h = ctypes.c_void_p()
+        explicit = None
+        if isinstance(row_order, str):
+            order_code = _capi.ORDERS[row_order]
+        else:
+            import numpy as np
+            explicit = np.ascontiguousarray(np.asarray(row_order), dtype=np.int32)
+            order_code = _capi.ORDERS["explicit"]
+        opts = _capi.PackOpts(int(blk_h), int(blk_w), _capi.PACKINGS[packing], _capi.DUPS[dup], order_code,
+                              explicit.ctypes.data if explicit is not None else None,
+                              int(explicit.shape[0]) if explicit is not None else 0, -1 if K is None else int(K))
         with torch.cuda.device(self.device):
             stream = _stream_handle(self.device) if on_dev else None
-            _capi.check(L.srbcrs_plan_create(_capi.ptr(rowptr), _capi.ptr(colind), _capi.ptr(values), int(num_nodes),
-                                             nnz, int(blk_h), int(blk_w), 1 if on_dev else 0, stream,
-                                             ctypes.byref(h)))
+            _capi.check(L.srbcrs_plan_create_ex(_capi.ptr(rowptr), _capi.ptr(colind), _capi.ptr(values),
+                                                int(num_nodes), nnz, ctypes.byref(opts), 1 if on_dev else 0, stream,
+                                                ctypes.byref(h)))
         self._h = h
         d = _capi.PlanDesc()
         _capi.check(L.srbcrs_plan_get(h, ctypes.byref(d)))
@@ -105,6 +124,14 @@ class Plan:
                                                   int(dense.stride(0)), out.data_ptr(), int(out.stride(0)),
                                                   int(out.shape[0]), ctypes.byref(opts), _stream_handle(self.device)))
         return out
+
+    def row_order(self):
+        """The plan's row order (new -> original) as a numpy array."""
+        import numpy as np
+        out = np.zeros(max(self.num_nodes, 1), dtype=np.int32)
+        n = ctypes.c_int32(0)
+        _capi.check(_capi.lib().srbcrs_plan_row_order(self._h, out.ctypes.data, self.num_nodes, ctypes.byref(n)))
+        return out[: n.value].copy()
 
     def block_values(self) -> Tensor:
         """The swizzled block values on the device (a copy)."""

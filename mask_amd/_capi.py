@@ -27,6 +27,7 @@ EXPORTS = (
     "srbcrs_plan_export_index", "srbcrs_plan_export_values",
     "srbcrs_schedule_build", "srbcrs_schedule_info", "srbcrs_schedule_export", "srbcrs_schedule_destroy",
     "srbcrs_plan_set_schedule", "srbcrs_run", "srbcrs_run_ex", "srbcrs_csr_spmm",
+    "srbcrs_row_order", "srbcrs_pack_count", "srbcrs_pack_fill", "srbcrs_plan_create_ex", "srbcrs_plan_row_order",
 )
 
 _i32p = ctypes.POINTER(ctypes.c_int32)
@@ -50,7 +51,22 @@ class PlanDesc(ctypes.Structure):
         ("d_soff", ctypes.c_void_p),
         ("d_sidx", ctypes.c_void_p),
         ("d_val", ctypes.c_void_p),
+        ("packed_rows", ctypes.c_int64),
+        ("d_row_map", ctypes.c_void_p),
+        ("packing", ctypes.c_int32),
+        ("dup_policy", ctypes.c_int32),
     ]
+
+
+class PackOpts(ctypes.Structure):
+    _fields_ = [("blk_h", ctypes.c_int32), ("blk_w", ctypes.c_int32), ("packing", ctypes.c_int32),
+                ("dup_policy", ctypes.c_int32), ("row_order", ctypes.c_int32), ("order", ctypes.c_void_p),
+                ("order_len", ctypes.c_int32), ("K", ctypes.c_int32)]
+
+
+ORDERS = {"identity": 0, "row_rcm": 1, "first_col_sort": 2, "jaccard_greedy": 3, "sparse_rows": 4, "explicit": 5}
+PACKINGS = {"column_condensed_dense": 0, "active_fixed_blocks_dense": 1}
+DUPS = {"last": 0, "sum": 1}
 
 
 class RunOpts(ctypes.Structure):
@@ -99,6 +115,12 @@ def lib() -> ctypes.CDLL:
         "srbcrs_run": ([_vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _vp], ctypes.c_int),
         "srbcrs_run_ex": ([_vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64, ctypes.POINTER(RunOpts), _vp],
                           ctypes.c_int),
+        "srbcrs_row_order": ([_vp, _vp, _i32, _i64, _i32, _i32, _vp, _i32p], ctypes.c_int),
+        "srbcrs_pack_count": ([_vp, _vp, _i32, _i64, ctypes.POINTER(PackOpts), _vp, _i64p], ctypes.c_int),
+        "srbcrs_pack_fill": ([_vp, _vp, _vp, _i32, _i64, ctypes.POINTER(PackOpts), _vp, _vp, _vp], ctypes.c_int),
+        "srbcrs_plan_create_ex": ([_vp, _vp, _vp, _i32, _i64, ctypes.POINTER(PackOpts), _i32, _vp,
+                                   ctypes.POINTER(_vp)], ctypes.c_int),
+        "srbcrs_plan_row_order": ([_vp, _vp, _i32, _i32p], ctypes.c_int),
         "srbcrs_csr_spmm": ([_vp, _vp, _vp, _i32, _i64, _i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp],
                             ctypes.c_int),
     }
@@ -171,3 +193,41 @@ def build_schedule(soff, policy: str, param: int = 0) -> dict:
         return out
     finally:
         L.srbcrs_schedule_destroy(h)
+
+
+def row_order_host(rowptr, colind, num_nodes: int, K: int, method: str) -> np.ndarray:
+    """The library's row order (new -> original) for `method`."""
+    L = lib()
+    rowptr = np.ascontiguousarray(rowptr, dtype=np.int32)
+    colind = np.ascontiguousarray(colind, dtype=np.int32)
+    out = np.zeros(max(num_nodes, 1), dtype=np.int32)
+    n = ctypes.c_int32(0)
+    check(L.srbcrs_row_order(ptr(rowptr), ptr(colind), num_nodes, int(colind.shape[0]), int(K), ORDERS[method],
+                             ptr(out), ctypes.byref(n)))
+    return out[: n.value].copy()
+
+
+def pack_host(rowptr, colind, values, num_nodes: int, K: int, order=None, blk_h: int = 16, blk_w: int = 8,
+              packing: str = "column_condensed_dense", dup: str = "sum") -> dict:
+    """The library's packer with an explicit (or identity) row order."""
+    L = lib()
+    rowptr = np.ascontiguousarray(rowptr, dtype=np.int32)
+    colind = np.ascontiguousarray(colind, dtype=np.int32)
+    values = np.ascontiguousarray(values, dtype=np.float32)
+    o = PackOpts(blk_h, blk_w, PACKINGS[packing], DUPS[dup], 0, None, 0, int(K))
+    rows = num_nodes
+    if order is not None:
+        order = np.ascontiguousarray(order, dtype=np.int32)
+        o.row_order, o.order, o.order_len = ORDERS["explicit"], order.ctypes.data, order.shape[0]
+        rows = order.shape[0]
+    nnz = int(colind.shape[0])
+    soff = np.zeros((rows + blk_h - 1) // blk_h + 1, dtype=np.int32)
+    total = ctypes.c_int64(0)
+    check(L.srbcrs_pack_count(ptr(rowptr), ptr(colind), num_nodes, nnz, ctypes.byref(o), ptr(soff),
+                              ctypes.byref(total)))
+    t = total.value
+    sidx = np.zeros(max(t * blk_w, 1), dtype=np.int32)
+    val = np.zeros(max(t * blk_h * blk_w, 1), dtype=np.float32)
+    check(L.srbcrs_pack_fill(ptr(rowptr), ptr(colind), ptr(values), num_nodes, nnz, ctypes.byref(o), ptr(soff),
+                             ptr(sidx), ptr(val)))
+    return dict(soff=soff, sidx=sidx[: t * blk_w], val=val[: t * blk_h * blk_w], total=t)

@@ -16,6 +16,7 @@
 
 #include "../../include/srbcrs.h"
 #include "srbcrs_kernels.h"
+#include "srbcrs_pack.h"
 
 namespace {
 
@@ -403,6 +404,14 @@ struct srbcrs_plan {
           *d_red_slot_off = nullptr;
   float* d_partial = nullptr;
   size_t partial_cap = 0;  // floats
+  // packing (generated-operator bridge): packed rows, row map, omitted rows
+  bool canonical = true;   // the preprocess_gpu conversion (edge maps available)
+  int32_t packing = 0, dup_policy = 0;
+  int64_t packed_rows = 0;
+  std::vector<int32_t> h_order;          // empty = identity
+  int32_t* d_rowmap = nullptr;
+  int32_t* d_zero_rows = nullptr;
+  int32_t n_zero_rows = 0;
 
   void free_schedule() {
     dev_free(d_group_off);
@@ -422,9 +431,117 @@ struct srbcrs_plan {
     dev_free(d_soff);
     dev_free(d_sidx);
     dev_free(d_val);
+    dev_free(d_rowmap);
+    dev_free(d_zero_rows);
     if (switched) (void)hipSetDevice(cur);
   }
 };
+
+namespace {
+
+void check_pack_opts(const srbcrs_pack_opts& o, int32_t num_nodes) {
+  if (o.packing != SRBCRS_PACK_CONDENSED && o.packing != SRBCRS_PACK_FIXED_BLOCKS)
+    fail(SRBCRS_EINVAL, "unknown packing %d", o.packing);
+  if (o.dup_policy != SRBCRS_DUP_LAST && o.dup_policy != SRBCRS_DUP_SUM)
+    fail(SRBCRS_EINVAL, "unknown duplicate policy %d", o.dup_policy);
+  if (o.row_order < SRBCRS_ORDER_IDENTITY || o.row_order > SRBCRS_ORDER_EXPLICIT)
+    fail(SRBCRS_EINVAL, "unknown row order %d", o.row_order);
+  if (o.packing == SRBCRS_PACK_FIXED_BLOCKS && o.K <= 0)
+    fail(SRBCRS_EINVAL, "fixed-block packing needs the column count K");
+  if (o.row_order == SRBCRS_ORDER_EXPLICIT) {
+    if (!o.order && o.order_len > 0) fail(SRBCRS_EINVAL, "explicit order is NULL");
+    if (o.order_len < 0 || o.order_len > num_nodes) fail(SRBCRS_EINVAL, "explicit order length out of range");
+    std::vector<uint8_t> seen((size_t)num_nodes, 0);
+    for (int32_t i = 0; i < o.order_len; ++i) {
+      const int32_t r = o.order[i];
+      if (r < 0 || r >= num_nodes || seen[r]) fail(SRBCRS_EINVAL, "explicit order must hold distinct rows in [0, num_nodes)");
+      seen[r] = 1;
+    }
+  }
+}
+
+srbcrs::PackSpec pack_spec(const srbcrs_pack_opts& o, int32_t num_nodes, const int32_t* order) {
+  srbcrs::PackSpec s;
+  s.blk_h = o.blk_h;
+  s.blk_w = o.blk_w;
+  s.packing = o.packing == SRBCRS_PACK_FIXED_BLOCKS ? srbcrs::kPackFixedBlocks : srbcrs::kPackCondensed;
+  s.dup_sum = o.dup_policy == SRBCRS_DUP_SUM;
+  s.order = (o.row_order == SRBCRS_ORDER_IDENTITY) ? nullptr : order;
+  s.rows = (o.row_order == SRBCRS_ORDER_IDENTITY) ? num_nodes : o.order_len;
+  s.K = o.K;
+  return s;
+}
+
+template <class F>
+auto guard_pack(F&& f) -> decltype(f()) {
+  try {
+    return f();
+  } catch (const std::out_of_range& e) {
+    fail(SRBCRS_EINVAL, "%s", e.what());
+  } catch (const std::overflow_error& e) {
+    fail(SRBCRS_EINVAL, "%s", e.what());
+  } catch (const std::invalid_argument& e) {
+    fail(SRBCRS_EINVAL, "%s", e.what());
+  }
+}
+
+std::vector<int32_t> compute_order(const int32_t* rowptr, const int32_t* colind, int32_t m, int32_t K,
+                                   int32_t method) {
+  int32_t k = K;
+  if (k < 0) {   // unknown column count: one past the largest column
+    k = 0;
+    for (int64_t e = rowptr[0]; e < rowptr[m]; ++e) k = std::max(k, colind[e] + 1);
+  }
+  return guard_pack([&] { return srbcrs::row_order(rowptr, colind, m, k, method); });
+}
+
+// A packed plan: resolve the order, pack on the host, upload arrays and the
+// row map, and list the output rows the order leaves out (zeroed per run).
+void create_packed(srbcrs_plan& plan, const int32_t* rp, const int32_t* ci, const float* vv,
+                   const srbcrs_pack_opts& o) {
+  const int32_t n = plan.num_nodes;
+  std::vector<int32_t> order;
+  if (o.row_order == SRBCRS_ORDER_EXPLICIT)
+    order.assign(o.order, o.order + o.order_len);
+  else
+    order = compute_order(rp, ci, n, o.K, o.row_order);
+  srbcrs_pack_opts eo = o;
+  eo.row_order = SRBCRS_ORDER_EXPLICIT;
+  eo.order = order.data();
+  eo.order_len = (int32_t)order.size();
+  srbcrs::PackSpec s = pack_spec(eo, n, order.data());
+  plan.packed_rows = (int64_t)order.size();
+  plan.Mo = (int32_t)((plan.packed_rows + plan.blk_h - 1) / plan.blk_h);
+  plan.h_soff.assign((size_t)plan.Mo + 1, 0);
+  plan.total = guard_pack([&] { return srbcrs::pack_count(rp, ci, s, plan.h_soff.data()); });
+  std::vector<int32_t> sidx((size_t)(plan.total * plan.blk_w));
+  std::vector<float> val((size_t)(plan.total * plan.blk_h * plan.blk_w));
+  guard_pack([&] {
+    srbcrs::pack_fill(rp, ci, vv, s, plan.h_soff.data(), sidx.data(), val.data());
+    return 0;
+  });
+  plan.max_col = -1;
+  for (int32_t c : sidx) plan.max_col = std::max(plan.max_col, c);
+  bool identity = (int64_t)order.size() == n;
+  for (int64_t i = 0; identity && i < (int64_t)order.size(); ++i) identity = order[i] == i;
+  if (!identity) {
+    plan.h_order = order;
+    plan.d_rowmap = upload(order);
+    std::vector<uint8_t> used((size_t)n, 0);
+    for (int32_t r : order) used[r] = 1;
+    std::vector<int32_t> zero;
+    for (int32_t r = 0; r < n; ++r)
+      if (!used[r]) zero.push_back(r);
+    plan.n_zero_rows = (int32_t)zero.size();
+    if (!zero.empty()) plan.d_zero_rows = upload(zero);
+  }
+  plan.d_soff = upload(plan.h_soff);
+  plan.d_sidx = upload(sidx);
+  plan.d_val = upload(val);
+  plan.sched.policy = "row";
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -464,10 +581,35 @@ int srbcrs_convert_fill(const int32_t* rowptr, const int32_t* colind, const floa
 int srbcrs_plan_create(const int32_t* rowptr, const int32_t* colind, const float* values,
                        int32_t num_nodes, int64_t nnz, int32_t blk_h, int32_t blk_w,
                        int32_t is_device, void* stream, srbcrs_plan** out) {
+  srbcrs_pack_opts o{};
+  o.blk_h = blk_h;
+  o.blk_w = blk_w;
+  o.packing = SRBCRS_PACK_CONDENSED;
+  o.dup_policy = SRBCRS_DUP_LAST;
+  o.row_order = SRBCRS_ORDER_IDENTITY;
+  o.K = -1;
+  return srbcrs_plan_create_ex(rowptr, colind, values, num_nodes, nnz, &o, is_device, stream, out);
+}
+
+int srbcrs_plan_create_ex(const int32_t* rowptr, const int32_t* colind, const float* values,
+                          int32_t num_nodes, int64_t nnz, const srbcrs_pack_opts* opts,
+                          int32_t is_device, void* stream, srbcrs_plan** out) {
   return guarded([&] {
     if (!out) fail(SRBCRS_EINVAL, "out is NULL");
     *out = nullptr;
+    srbcrs_pack_opts o{};
+    if (opts) {
+      o = *opts;
+    } else {
+      o.blk_h = 16;
+      o.blk_w = 8;
+      o.K = -1;
+    }
+    const int32_t blk_h = o.blk_h, blk_w = o.blk_w;
     check_block_shape(blk_h, blk_w);
+    check_pack_opts(o, num_nodes);
+    const bool canonical = o.packing == SRBCRS_PACK_CONDENSED && o.dup_policy == SRBCRS_DUP_LAST &&
+                           o.row_order == SRBCRS_ORDER_IDENTITY;
     if (num_nodes < 1) fail(SRBCRS_EINVAL, "num_nodes must be positive");
     if (nnz < 0 || nnz > INT32_MAX) fail(SRBCRS_EINVAL, "nnz out of range");
     std::vector<int32_t> h_rowptr, h_colind;
@@ -498,8 +640,17 @@ int srbcrs_plan_create(const int32_t* rowptr, const int32_t* colind, const float
     plan->num_nodes = num_nodes;
     plan->blk_h = blk_h;
     plan->blk_w = blk_w;
-    plan->Mo = (num_nodes + blk_h - 1) / blk_h;
     plan->nnz = nnz;
+    plan->packing = o.packing;
+    plan->dup_policy = o.dup_policy;
+    plan->canonical = canonical;
+    if (!canonical) {
+      create_packed(*plan, rp, ci, vv, o);
+      *out = plan.release();
+      return;
+    }
+    plan->packed_rows = num_nodes;
+    plan->Mo = (num_nodes + blk_h - 1) / blk_h;
     Uniq u;
     build_uniq(rp, ci, num_nodes, blk_h, u);
     plan->max_col = u.max_col;
@@ -537,6 +688,69 @@ int srbcrs_plan_get(const srbcrs_plan* plan, srbcrs_plan_desc* out) {
     out->d_soff = plan->d_soff;
     out->d_sidx = plan->d_sidx;
     out->d_val = plan->d_val;
+    out->packed_rows = plan->packed_rows;
+    out->d_row_map = plan->d_rowmap;
+    out->packing = plan->packing;
+    out->dup_policy = plan->dup_policy;
+  });
+}
+
+int srbcrs_plan_row_order(const srbcrs_plan* plan, int32_t* order, int32_t capacity, int32_t* len) {
+  return guarded([&] {
+    if (!plan || !len) fail(SRBCRS_EINVAL, "plan / len is NULL");
+    *len = (int32_t)plan->packed_rows;
+    if (!order) return;
+    if (capacity < plan->packed_rows) fail(SRBCRS_EINVAL, "order buffer too short");
+    if (plan->h_order.empty())
+      for (int64_t i = 0; i < plan->packed_rows; ++i) order[i] = (int32_t)i;
+    else
+      std::memcpy(order, plan->h_order.data(), plan->h_order.size() * 4);
+  });
+}
+
+int srbcrs_row_order(const int32_t* rowptr, const int32_t* colind, int32_t num_nodes, int64_t nnz,
+                     int32_t K, int32_t method, int32_t* order, int32_t* order_len) {
+  return guarded([&] {
+    check_csr(rowptr, colind, num_nodes, nnz);
+    if (!order || !order_len) fail(SRBCRS_EINVAL, "order / order_len is NULL");
+    if (method < SRBCRS_ORDER_IDENTITY || method > SRBCRS_ORDER_SPARSE_ROWS)
+      fail(SRBCRS_EINVAL, "unknown row order method %d", method);
+    std::vector<int32_t> o = compute_order(rowptr, colind, num_nodes, K, method);
+    std::memcpy(order, o.data(), o.size() * 4);
+    *order_len = (int32_t)o.size();
+  });
+}
+
+int srbcrs_pack_count(const int32_t* rowptr, const int32_t* colind, int32_t num_nodes, int64_t nnz,
+                      const srbcrs_pack_opts* opts, int32_t* soff, int64_t* total_tiles) {
+  return guarded([&] {
+    check_csr(rowptr, colind, num_nodes, nnz);
+    if (!opts || !soff || !total_tiles) fail(SRBCRS_EINVAL, "NULL argument");
+    check_block_shape(opts->blk_h, opts->blk_w);
+    check_pack_opts(*opts, num_nodes);
+    if (opts->row_order != SRBCRS_ORDER_IDENTITY && opts->row_order != SRBCRS_ORDER_EXPLICIT)
+      fail(SRBCRS_EINVAL, "pack_count takes an identity or explicit order (use srbcrs_row_order)");
+    srbcrs::PackSpec s = pack_spec(*opts, num_nodes, opts->order);
+    *total_tiles = guard_pack([&] { return srbcrs::pack_count(rowptr, colind, s, soff); });
+  });
+}
+
+int srbcrs_pack_fill(const int32_t* rowptr, const int32_t* colind, const float* values,
+                     int32_t num_nodes, int64_t nnz, const srbcrs_pack_opts* opts,
+                     const int32_t* soff, int32_t* sidx, float* val) {
+  return guarded([&] {
+    check_csr(rowptr, colind, num_nodes, nnz);
+    if (!opts || !soff || !sidx || !val) fail(SRBCRS_EINVAL, "NULL argument");
+    if (nnz > 0 && !values) fail(SRBCRS_EINVAL, "values is NULL");
+    check_block_shape(opts->blk_h, opts->blk_w);
+    check_pack_opts(*opts, num_nodes);
+    if (opts->row_order != SRBCRS_ORDER_IDENTITY && opts->row_order != SRBCRS_ORDER_EXPLICIT)
+      fail(SRBCRS_EINVAL, "pack_fill takes an identity or explicit order (use srbcrs_row_order)");
+    srbcrs::PackSpec s = pack_spec(*opts, num_nodes, opts->order);
+    guard_pack([&] {
+      srbcrs::pack_fill(rowptr, colind, values, s, soff, sidx, val);
+      return 0;
+    });
   });
 }
 
@@ -546,6 +760,7 @@ int srbcrs_plan_write_edges(const srbcrs_plan* plan, int32_t* d_block_partition,
                             int64_t edge_to_row_len, void* stream) {
   return guarded([&] {
     if (!plan) fail(SRBCRS_EINVAL, "plan is NULL");
+    if (!plan->canonical) fail(SRBCRS_EINVAL, "edge maps exist only for canonical (preprocess_gpu) plans");
     hipStream_t st = static_cast<hipStream_t>(stream);
     if (d_block_partition && block_partition_len >= plan->Mo && plan->Mo > 0)
       hip_check(hipMemcpyAsync(d_block_partition, plan->h_block_partition.data(), (size_t)plan->Mo * 4,
@@ -704,8 +919,11 @@ int srbcrs_run_ex(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int
                        (reinterpret_cast<uintptr_t>(d_B) % (4 * vec)) ||
                        (reinterpret_cast<uintptr_t>(d_C) % (4 * vec))))
       vec /= 2;
-    srbcrs::StreamArgs a{d_B, d_C, nullptr, plan->d_sidx, plan->d_val, plan->num_nodes, (int)N, ldb, ldc,
-                         plan->blk_h};
+    srbcrs::StreamArgs a{d_B, d_C, nullptr, plan->d_sidx, plan->d_val, (int)plan->packed_rows, (int)N, ldb, ldc,
+                         plan->blk_h, plan->d_rowmap};
+    if (plan->n_zero_rows)
+      hip_check(srbcrs::launch_zero_rows(d_C, plan->d_zero_rows, plan->n_zero_rows, (int)N, ldc, st),
+                "launch zero_rows");
     if (plan->sched.policy == "row") {
       hip_check(srbcrs::launch_row(a, plan->d_soff, plan->Mo, vec, ro, st), "launch spmm_stream(row)");
       return;
@@ -724,7 +942,8 @@ int srbcrs_run_ex(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int
                          plan->d_task_slot, (int)s.group_off.size() - 1};
     hip_check(srbcrs::launch_tasks(a, tt, vec, ro, st), "launch spmm_stream(tasks)");
     srbcrs::ReduceArgs ra{plan->d_partial, d_C, plan->d_red_window, plan->d_red_slot_off,
-                          (int)s.red_window.size(), plan->blk_h, plan->num_nodes, (int)N, ldc};
+                          (int)s.red_window.size(), plan->blk_h, (int)plan->packed_rows, (int)N, ldc,
+                          plan->d_rowmap};
     hip_check(srbcrs::launch_reduce(ra, vec, st), "launch segment_reduce");
   });
 }

@@ -25,6 +25,7 @@ struct StreamArgs {
   int M, N;
   int64_t ldb, ldc;
   int blk_h;        // 16 (16x8 blocks) or 32 (32x32 blocks)
+  const int* rowmap = nullptr;  // packed row -> output row (null = identity); M counts packed rows
 };
 
 struct TaskTable {
@@ -43,8 +44,9 @@ struct ReduceArgs {
   const int* red_slot_off;
   int n_red;
   int tile_rows;    // rows per window (the block height)
-  int M, N;
+  int M, N;         // M counts packed rows
   int64_t ldc;
+  const int* rowmap = nullptr;
 };
 
 struct CsrArgs {
@@ -63,5 +65,6 @@ hipError_t launch_tasks(const StreamArgs& a, const TaskTable& t, int vec, const 
                         hipStream_t st);
 hipError_t launch_reduce(const ReduceArgs& a, int vec, hipStream_t st);
 hipError_t launch_csr(const CsrArgs& a, int vec, hipStream_t st);
+hipError_t launch_zero_rows(float* C, const int* rows, int n_rows, int N, int64_t ldc, hipStream_t st);
 
 }  // namespace srbcrs

@@ -75,13 +75,13 @@ static hipError_t launch_src(const Src& src, int n_groups, const StreamArgs& a, 
 hipError_t launch_row(const StreamArgs& a, const int* soff, int Mo, int vec, const RunOpts& o,
                       hipStream_t st) {
   const int wpw = o.windows_per_wave > 0 ? o.windows_per_wave : 1;
-  RowTasks src{soff, Mo, wpw};
+  RowTasks src{soff, Mo, wpw, a.rowmap};
   return launch_src(src, (Mo + wpw - 1) / wpw, a, vec, o, st);
 }
 
 hipError_t launch_tasks(const StreamArgs& a, const TaskTable& t, int vec, const RunOpts& o,
                         hipStream_t st) {
-  TableTasks src{t.group_off, t.task_begin, t.task_end, t.task_window, t.task_slot};
+  TableTasks src{t.group_off, t.task_begin, t.task_end, t.task_window, t.task_slot, a.rowmap};
   return launch_src(src, t.n_groups, a, vec, o, st);
 }
 
@@ -92,13 +92,13 @@ hipError_t launch_reduce(const ReduceArgs& a, int vec, hipStream_t st) {
   if (blocks > 65536) blocks = 65536;
   if (vec == 4)
     hipLaunchKernelGGL(segment_reduce<4>, dim3((unsigned)blocks), dim3(256), 0, st, a.partial, a.C,
-                       a.red_window, a.red_slot_off, a.n_red, a.tile_rows, a.M, a.N, a.ldc);
+                       a.red_window, a.red_slot_off, a.n_red, a.tile_rows, a.M, a.N, a.ldc, a.rowmap);
   else if (vec == 2)
     hipLaunchKernelGGL(segment_reduce<2>, dim3((unsigned)blocks), dim3(256), 0, st, a.partial, a.C,
-                       a.red_window, a.red_slot_off, a.n_red, a.tile_rows, a.M, a.N, a.ldc);
+                       a.red_window, a.red_slot_off, a.n_red, a.tile_rows, a.M, a.N, a.ldc, a.rowmap);
   else
     hipLaunchKernelGGL(segment_reduce<1>, dim3((unsigned)blocks), dim3(256), 0, st, a.partial, a.C,
-                       a.red_window, a.red_slot_off, a.n_red, a.tile_rows, a.M, a.N, a.ldc);
+                       a.red_window, a.red_slot_off, a.n_red, a.tile_rows, a.M, a.N, a.ldc, a.rowmap);
   return hipGetLastError();
 }
 
@@ -116,6 +116,15 @@ hipError_t launch_csr(const CsrArgs& a, int vec, hipStream_t st) {
   else
     hipLaunchKernelGGL((csr_spmm_rowwave<1, 4>), grid, dim3(256), 0, st, a.rowptr, a.colind,
                        a.values, a.B, a.C, a.M, a.N, a.ldb, a.ldc);
+  return hipGetLastError();
+}
+
+hipError_t launch_zero_rows(float* C, const int* rows, int n_rows, int N, int64_t ldc, hipStream_t st) {
+  if (n_rows == 0 || N == 0) return hipSuccess;
+  const int64_t total = (int64_t)n_rows * N;
+  int64_t blocks = (total + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(zero_rows, dim3((unsigned)blocks), dim3(256), 0, st, C, rows, n_rows, N, ldc);
   return hipGetLastError();
 }
 

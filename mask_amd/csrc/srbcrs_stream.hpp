@@ -128,19 +128,22 @@ __device__ __forceinline__ void mma_frag(const Frag<H, VEC, G>& f, f4 (&acc)[H][
       }
 }
 
-// Store a 16 x (16*VEC*G) accumulator tile.  row0 is the tile's first row in
-// `out`, rows >= row_limit are skipped (M % 16 != 0).
+// Store a 16 x (16*VEC*G) accumulator tile.  row0 is the tile's first
+// (packed) row, rows >= row_limit are skipped (M % 16 != 0).  With a row map
+// packed row p is written to output row rowmap[p] (reordered or sparse-row
+// packings); the map is applied here, in the store, not in a separate pass.
 template <int VEC, int G>
 __device__ __forceinline__ void store_tile(const f4 (&acc)[G][VEC], float* __restrict__ out,
                                            int64_t row0, int64_t row_limit, int64_t ldc, int col0,
-                                           int lane) {
+                                           int lane, const int* __restrict__ rowmap = nullptr) {
   typedef typename VecT<VEC>::type V;
   const int k = lane >> 4;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int64_t row = row0 + 4 * k + r;
     if (row < row_limit) {
-      float* p = out + row * ldc + col0;
+      const int64_t orow = rowmap ? (int64_t)rowmap[row] : row;
+      float* p = out + orow * ldc + col0;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         V v;
@@ -166,6 +169,7 @@ struct RowTasks {
   const int* __restrict__ soff;
   int Mo;
   int wpw;
+  const int* __restrict__ rowmap = nullptr;   // packed row -> output row (null = identity)
   __device__ __forceinline__ void group(int g, int& t0, int& t1) const {
     t0 = g * wpw;
     t1 = t0 + wpw < Mo ? t0 + wpw : Mo;
@@ -183,6 +187,7 @@ struct TableTasks {
   const int* __restrict__ task_end;
   const int* __restrict__ task_window;
   const int* __restrict__ task_slot;
+  const int* __restrict__ rowmap = nullptr;   // packed row -> output row (null = identity)
   __device__ __forceinline__ void group(int g, int& t0, int& t1) const {
     t0 = group_off[g];
     t1 = group_off[g + 1];
@@ -201,7 +206,7 @@ __device__ __forceinline__ void flush_task(const Src& src, int t, f4 (&acc)[BH /
 #pragma unroll
   for (int h = 0; h < BH / 16; ++h) {
     if (slot < 0)
-      store_tile<VEC, G>(acc[h], C, (int64_t)src.window(t) * BH + 16 * h, M, ldc, col0, lane);
+      store_tile<VEC, G>(acc[h], C, (int64_t)src.window(t) * BH + 16 * h, M, ldc, col0, lane, src.rowmap);
     else
       store_tile<VEC, G>(acc[h], partial, (int64_t)slot * BH + 16 * h, (int64_t)(slot + 1) * BH, ldc,
                          col0, lane);
@@ -299,14 +304,15 @@ __global__ __launch_bounds__(64 * WAVES) void spmm_stream(
 // order (deterministic; zero slots give zeros).  The atomic-free
 // counterpart of the reference's reduce_tcf_segments
 // (examples/src_fp32/acc/testbed/custom_format_e2e.cu:832-853).  One thread
-// per VEC consecutive columns.
+// per VEC consecutive columns.  M counts packed rows; rowmap (or null) maps
+// them to output rows as in store_tile.
 template <int VEC>
 __global__ __launch_bounds__(256) void segment_reduce(const float* __restrict__ partial,
                                                       float* __restrict__ C,
                                                       const int* __restrict__ red_window,
                                                       const int* __restrict__ red_slot_off,
                                                       int n_red, int tile_rows, int M, int N,
-                                                      int64_t ldc) {
+                                                      int64_t ldc, const int* __restrict__ rowmap) {
   typedef typename VecT<VEC>::type V;
   const int64_t nv = N / VEC;
   const int64_t per = tile_rows * nv;
@@ -323,7 +329,19 @@ __global__ __launch_bounds__(256) void segment_reduce(const float* __restrict__ 
     if constexpr (VEC == 1) s = 0.f; else { for (int q = 0; q < VEC; ++q) s[q] = 0.f; }
     for (int sl = red_slot_off[i]; sl < red_slot_off[i + 1]; ++sl)
       s += *reinterpret_cast<const V*>(partial + ((int64_t)sl * tile_rows + r) * ldc + VEC * cv);
-    *reinterpret_cast<V*>(C + row * ldc + VEC * cv) = s;
+    const int64_t orow = rowmap ? (int64_t)rowmap[row] : row;
+    *reinterpret_cast<V*>(C + orow * ldc + VEC * cv) = s;
+  }
+}
+
+// Zero the listed output rows (rows a sparse-row packing leaves out).
+__global__ __launch_bounds__(256) void zero_rows(float* __restrict__ C, const int* __restrict__ rows,
+                                                 int n_rows, int N, int64_t ldc) {
+  const int64_t total = (int64_t)n_rows * N;
+  for (int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; id < total;
+       id += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i = id / N, c = id % N;
+    C[(int64_t)rows[i] * ldc + c] = 0.f;
   }
 }
 

@@ -172,12 +172,13 @@ extern "C" const char* sparsene_generated_metadata(void) {{
   return R"JSON({metadata})JSON";
 }}
 
-// C[0:M] = A * B over the row schedule (one task per BH-row window).
+// C = A * B over the row schedule (one task per BH-row window).  M counts
+// packed rows; rowmap (or null) sends packed row p to output row rowmap[p].
 extern "C" int sparsene_generated_run(const float* B, float* C, const int* soff, const int* sidx,
                                       const float* val, int M, int N, int Mo, long long ldb,
-                                      long long ldc, void* stream) {{
+                                      long long ldc, const int* rowmap, void* stream) {{
   if (operand_check(B, C, N, ldb, ldc)) return -1;
-  srbcrs::RowTasks src{{soff, Mo, 1}};
+  srbcrs::RowTasks src{{soff, Mo, 1, rowmap}};
   return launch(src, Mo, B, C, nullptr, sidx, val, M, N, ldb, ldc, static_cast<hipStream_t>(stream));
 }}
 
@@ -187,16 +188,16 @@ extern "C" int sparsene_generated_run_tasks(const float* B, float* C, float* par
                                             const int* task_begin, const int* task_end,
                                             const int* task_window, const int* task_slot,
                                             int n_groups, int M, int N, long long ldb,
-                                            long long ldc, void* stream) {{
+                                            long long ldc, const int* rowmap, void* stream) {{
   if (operand_check(B, C, N, ldb, ldc)) return -1;
-  srbcrs::TableTasks src{{group_off, task_begin, task_end, task_window, task_slot}};
+  srbcrs::TableTasks src{{group_off, task_begin, task_end, task_window, task_slot, rowmap}};
   return launch(src, n_groups, B, C, partial, sidx, val, M, N, ldb, ldc, static_cast<hipStream_t>(stream));
 }}
 
 // Deterministic reduction of the partial tiles into C (tile_rows = BH).
 extern "C" int sparsene_generated_reduce(const float* partial, float* C, const int* red_window,
                                          const int* red_slot_off, int n_red, int M, int N,
-                                         long long ldc, void* stream) {{
+                                         long long ldc, const int* rowmap, void* stream) {{
   if (n_red == 0) return 0;
   if (N % kVEC || ldc % kVEC) return -1;
   long long total = (long long)n_red * kBH * (N / kVEC);
@@ -204,7 +205,19 @@ extern "C" int sparsene_generated_reduce(const float* partial, float* C, const i
   if (blocks > 65536) blocks = 65536;
   hipLaunchKernelGGL(srbcrs::segment_reduce<kVEC>, dim3((unsigned)blocks), dim3(256), 0,
                      static_cast<hipStream_t>(stream), partial, C, red_window, red_slot_off, n_red, kBH,
-                     M, N, (int64_t)ldc);
+                     M, N, (int64_t)ldc, rowmap);
+  return hipGetLastError() == hipSuccess ? 0 : -2;
+}}
+
+// Zero the output rows a sparse-row packing leaves out.
+extern "C" int sparsene_generated_zero_rows(float* C, const int* rows, int n_rows, int N, long long ldc,
+                                            void* stream) {{
+  if (n_rows == 0 || N == 0) return 0;
+  long long total = (long long)n_rows * N;
+  long long blocks = (total + 255) / 256;
+  if (blocks > 65536) blocks = 65536;
+  hipLaunchKernelGGL(srbcrs::zero_rows, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     C, rows, n_rows, N, (int64_t)ldc);
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }}
 """
@@ -294,12 +307,14 @@ class GeneratedOperator:
         L = ctypes.CDLL(str(self.path))
         vp, i32, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong
         L.sparsene_generated_metadata.restype = ctypes.c_char_p
-        L.sparsene_generated_run.argtypes = [vp] * 5 + [i32, i32, i32, i64, i64, vp]
+        L.sparsene_generated_run.argtypes = [vp] * 5 + [i32, i32, i32, i64, i64, vp, vp]
         L.sparsene_generated_run.restype = ctypes.c_int
-        L.sparsene_generated_run_tasks.argtypes = [vp] * 10 + [i32, i32, i32, i64, i64, vp]
+        L.sparsene_generated_run_tasks.argtypes = [vp] * 10 + [i32, i32, i32, i64, i64, vp, vp]
         L.sparsene_generated_run_tasks.restype = ctypes.c_int
-        L.sparsene_generated_reduce.argtypes = [vp] * 4 + [i32, i32, i32, i64, vp]
+        L.sparsene_generated_reduce.argtypes = [vp] * 4 + [i32, i32, i32, i64, vp, vp]
         L.sparsene_generated_reduce.restype = ctypes.c_int
+        L.sparsene_generated_zero_rows.argtypes = [vp, vp, i32, i32, i64, vp]
+        L.sparsene_generated_zero_rows.restype = ctypes.c_int
         self._lib = L
         self.metadata = json.loads(L.sparsene_generated_metadata().decode())
         self.params = KernelParams(**self.metadata["kernel_params"])
@@ -325,10 +340,22 @@ class GeneratedOperator:
             p95 = int(np.sort(lens)[min(lens.size - 1, max(0, int(np.ceil(lens.size * 0.95)) - 1))]) if lens.size else 0
             pol = "strict_lb" if lens.size and lens.max() > max(64, 4 * max(p95, 1)) else "row"
         N = int(dense.shape[1])
+        P = int(d.packed_rows)
+        zk = ("zero", id(plan))
+        if zk not in self._tables:
+            order = plan.row_order()
+            mask = np.ones(plan.num_nodes, bool)
+            mask[order] = False
+            self._tables[zk] = (torch.from_numpy(np.nonzero(mask)[0].astype(np.int32)).to(dense.device), plan)
+        zero = self._tables[zk][0]
+        if zero.numel():
+            if self._lib.sparsene_generated_zero_rows(out.data_ptr(), zero.data_ptr(), zero.numel(), N,
+                                                      out.stride(0), st):
+                raise RuntimeError("generated zero-fill failed")
         if pol == "row":
             rc = self._lib.sparsene_generated_run(dense.data_ptr(), out.data_ptr(), d.d_soff, d.d_sidx, d.d_val,
-                                                  plan.num_nodes, N, plan.row_windows, dense.stride(0),
-                                                  out.stride(0), st)
+                                                  P, N, plan.row_windows, dense.stride(0),
+                                                  out.stride(0), d.d_row_map, st)
             if rc:
                 raise RuntimeError(f"generated operator rejected the operands (status {rc})")
             return out
@@ -344,12 +371,12 @@ class GeneratedOperator:
         rc = self._lib.sparsene_generated_run_tasks(
             dense.data_ptr(), out.data_ptr(), partial.data_ptr(), d.d_sidx, d.d_val, dev["group_off"].data_ptr(),
             dev["task_begin"].data_ptr(), dev["task_end"].data_ptr(), dev["task_window"].data_ptr(),
-            dev["task_slot"].data_ptr(), tab["group_off"].size - 1, plan.num_nodes, N, dense.stride(0), N, st)
+            dev["task_slot"].data_ptr(), tab["group_off"].size - 1, P, N, dense.stride(0), N, d.d_row_map, st)
         if rc:
             raise RuntimeError(f"generated operator rejected the operands (status {rc})")
         rc = self._lib.sparsene_generated_reduce(partial.data_ptr(), out.data_ptr(), dev["red_window"].data_ptr(),
                                                  dev["red_slot_off"].data_ptr(), tab["red_window"].size,
-                                                 plan.num_nodes, N, N, st)
+                                                 P, N, N, d.d_row_map, st)
         if rc:
             raise RuntimeError(f"generated reduction failed (status {rc})")
         return out

@@ -61,6 +61,20 @@ def _load():
     lib.oracle_segment_auto.restype = ctypes.c_int
     lib.oracle_segment_reduce.argtypes = [_f32p, _f32p, _i32p, ctypes.c_int, ctypes.c_int, ctypes.c_int]
     lib.oracle_segment_reduce.restype = None
+    lib.oracle_order_first_col.argtypes = [ctypes.c_int, ctypes.c_int, _i32p, _i32p, _i32p]
+    lib.oracle_order_first_col.restype = None
+    lib.oracle_order_rcm.argtypes = [ctypes.c_int, ctypes.c_int, _i32p, _i32p, _i32p]
+    lib.oracle_order_rcm.restype = ctypes.c_int
+    lib.oracle_order_jaccard.argtypes = [ctypes.c_int, ctypes.c_int, _i32p, _i32p, _i32p]
+    lib.oracle_order_jaccard.restype = None
+    lib.oracle_order_sparse_rows.argtypes = [ctypes.c_int, _i32p, _i32p]
+    lib.oracle_order_sparse_rows.restype = ctypes.c_int
+    lib.oracle_pack_count.argtypes = [_i32p, _i32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _i32p,
+                                      ctypes.c_int, _i32p]
+    lib.oracle_pack_count.restype = ctypes.c_int64
+    lib.oracle_pack_fill.argtypes = [_i32p, _i32p, _f32p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                     _i32p, ctypes.c_int, _i32p, _i32p, _f32p]
+    lib.oracle_pack_fill.restype = None
     _lib = lib
     return lib
 
@@ -188,6 +202,53 @@ def segment_reduce(partial, win_seg_off, tile_rows: int, n: int):
     out = np.zeros((mo * tile_rows, n), dtype=np.float32)
     lib.oracle_segment_reduce(_p(partial, _f32p), _p(out, _f32p), _p(wso, _i32p), mo, tile_rows, n)
     return out
+
+
+def row_order(rowptr, colind, m: int, k: int, method: str) -> np.ndarray:
+    """Row orders new -> original (custom_format_e2e.cu:157-349, 483-488):
+    "row_rcm", "first_col_sort", "jaccard_greedy", "sparse_rows", "identity"."""
+    lib = _load()
+    rowptr = np.ascontiguousarray(rowptr, dtype=np.int32)
+    colind = np.ascontiguousarray(colind, dtype=np.int32)
+    out = np.zeros(max(m, 1), dtype=np.int32)
+    if method == "identity":
+        return np.arange(m, dtype=np.int32)
+    if method == "first_col_sort":
+        lib.oracle_order_first_col(m, k, _p(rowptr, _i32p), _p(colind, _i32p), _p(out, _i32p))
+    elif method == "row_rcm":
+        if lib.oracle_order_rcm(m, k, _p(rowptr, _i32p), _p(colind, _i32p), _p(out, _i32p)) != 0:
+            raise ValueError("row_rcm currently requires a square matrix")
+    elif method == "jaccard_greedy":
+        lib.oracle_order_jaccard(m, k, _p(rowptr, _i32p), _p(colind, _i32p), _p(out, _i32p))
+    elif method == "sparse_rows":
+        n = lib.oracle_order_sparse_rows(m, _p(rowptr, _i32p), _p(out, _i32p))
+        return out[:n].copy()
+    else:
+        raise ValueError(method)
+    return out[:m].copy()
+
+
+def pack(rowptr, colind, values, k: int, order, blk_h: int = 16, blk_w: int = 8, packing: int = 0) -> dict:
+    """Generated-operator packing (custom_format_e2e.cu:496-640): rows in
+    `order`, duplicates summed; packing 0 = column-condensed dense, 1 =
+    active fixed blocks dense."""
+    lib = _load()
+    rowptr = np.ascontiguousarray(rowptr, dtype=np.int32)
+    colind = np.ascontiguousarray(colind, dtype=np.int32)
+    values = np.ascontiguousarray(values, dtype=np.float32)
+    order = np.ascontiguousarray(order, dtype=np.int32)
+    P = int(order.shape[0])
+    W = (P + blk_h - 1) // blk_h
+    soff = np.zeros(W + 1, dtype=np.int32)
+    total = int(lib.oracle_pack_count(_p(rowptr, _i32p), _p(colind, _i32p), k, blk_h, blk_w, packing,
+                                      _p(order, _i32p), P, _p(soff, _i32p)))
+    if total < 0:
+        raise ValueError("CSR column index out of range")
+    sidx = np.zeros(max(total * blk_w, 1), dtype=np.int32)
+    val = np.zeros(max(total * blk_h * blk_w, 1), dtype=np.float32)
+    lib.oracle_pack_fill(_p(rowptr, _i32p), _p(colind, _i32p), _p(values, _f32p), k, blk_h, blk_w, packing,
+                         _p(order, _i32p), P, _p(soff, _i32p), _p(sidx, _i32p), _p(val, _f32p))
+    return dict(soff=soff, sidx=sidx[: total * blk_w], val=val[: total * blk_h * blk_w], total=total)
 
 
 def error_metrics(C, C64, absAB):

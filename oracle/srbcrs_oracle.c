@@ -321,3 +321,262 @@ void oracle_segment_reduce(const float *partial, float *out, const int *win_seg_
       out[(int64_t)w * te + i] = s;
     }
 }
+
+/* ===== generated-operator packing (CFE = custom_format_e2e.cu) ============ */
+
+static int cmp_key2(const void *a, const void *b) {
+  const int64_t *x = (const int64_t *)a, *y = (const int64_t *)b;
+  if (x[0] != y[0]) return (x[0] > y[0]) - (x[0] < y[0]);
+  return (x[1] > y[1]) - (x[1] < y[1]);
+}
+
+/* first_structural_column (CFE:228-234): min column in [0,k), k if none. */
+static int first_col(int row, int k, const int *rowptr, const int *colind) {
+  int f = k;
+  for (int p = rowptr[row]; p < rowptr[row + 1]; ++p)
+    if (colind[p] >= 0 && colind[p] < k && colind[p] < f) f = colind[p];
+  return f;
+}
+
+/* first_column_order (CFE:236-249): stable sort by (first column, row). */
+void oracle_order_first_col(int m, int k, const int *rowptr, const int *colind, int *order) {
+  int64_t *key = (int64_t *)malloc(sizeof(int64_t) * 2 * (size_t)(m > 0 ? m : 1));
+  for (int r = 0; r < m; ++r) { key[2 * r] = first_col(r, k, rowptr, colind); key[2 * r + 1] = r; }
+  qsort(key, (size_t)m, 2 * sizeof(int64_t), cmp_key2);
+  for (int r = 0; r < m; ++r) order[r] = (int)key[2 * r + 1];
+  free(key);
+}
+
+/* reverse_cuthill_mckee (CFE:163-226), square matrices: symmetrised
+ * adjacency without self loops, degree = unique neighbours; components are
+ * started from nodes in (degree, id) order; BFS appends each popped node's
+ * unvisited neighbours in (degree, id) order; each component is reversed.
+ * Returns 0, or -1 if m != k. */
+int oracle_order_rcm(int m, int k, const int *rowptr, const int *colind, int *order) {
+  if (m != k) return -1;
+  int64_t ne = 0;
+  for (int r = 0; r < m; ++r)
+    for (int p = rowptr[r]; p < rowptr[r + 1]; ++p)
+      if (colind[p] >= 0 && colind[p] < m && colind[p] != r) ne += 2;
+  int64_t *pairs = (int64_t *)malloc(sizeof(int64_t) * 2 * (size_t)(ne > 0 ? ne : 1));
+  int64_t q = 0;
+  for (int r = 0; r < m; ++r)
+    for (int p = rowptr[r]; p < rowptr[r + 1]; ++p) {
+      int c = colind[p];
+      if (c < 0 || c >= m || c == r) continue;
+      pairs[2 * q] = r; pairs[2 * q + 1] = c; ++q;
+      pairs[2 * q] = c; pairs[2 * q + 1] = r; ++q;
+    }
+  qsort(pairs, (size_t)ne, 2 * sizeof(int64_t), cmp_key2);
+  int64_t *adj_off = (int64_t *)calloc((size_t)m + 1, sizeof(int64_t));
+  int *adj = (int *)malloc(sizeof(int) * (size_t)(ne > 0 ? ne : 1));
+  int64_t na = 0;
+  for (int64_t i = 0; i < ne; ++i) {
+    if (i > 0 && pairs[2 * i] == pairs[2 * i - 2] && pairs[2 * i + 1] == pairs[2 * i - 1]) continue;
+    adj[na++] = (int)pairs[2 * i + 1];
+    adj_off[pairs[2 * i] + 1]++;
+  }
+  for (int r = 0; r < m; ++r) adj_off[r + 1] += adj_off[r];
+  int *deg = (int *)malloc(sizeof(int) * (size_t)(m > 0 ? m : 1));
+  for (int r = 0; r < m; ++r) deg[r] = (int)(adj_off[r + 1] - adj_off[r]);
+  int64_t *key = (int64_t *)malloc(sizeof(int64_t) * 2 * (size_t)(m > 0 ? m : 1));
+  for (int r = 0; r < m; ++r) { key[2 * r] = deg[r]; key[2 * r + 1] = r; }
+  qsort(key, (size_t)m, 2 * sizeof(int64_t), cmp_key2);
+  unsigned char *vis = (unsigned char *)calloc((size_t)(m > 0 ? m : 1), 1);
+  int *queue = (int *)malloc(sizeof(int) * (size_t)(m > 0 ? m : 1));
+  int64_t *nk = (int64_t *)malloc(sizeof(int64_t) * 2 * (size_t)(m > 0 ? m : 1));
+  int out = 0;
+  for (int s = 0; s < m; ++s) {
+    int start = (int)key[2 * s + 1];
+    if (vis[start]) continue;
+    int head = 0, tail = 0;
+    vis[start] = 1;
+    queue[tail++] = start;
+    while (head < tail) {
+      int row = queue[head++];
+      int nn = 0;
+      for (int64_t p = adj_off[row]; p < adj_off[row + 1]; ++p)
+        if (!vis[adj[p]]) { nk[2 * nn] = deg[adj[p]]; nk[2 * nn + 1] = adj[p]; ++nn; }
+      qsort(nk, (size_t)nn, 2 * sizeof(int64_t), cmp_key2);
+      for (int i = 0; i < nn; ++i) {
+        int v = (int)nk[2 * i + 1];
+        if (!vis[v]) { vis[v] = 1; queue[tail++] = v; }
+      }
+    }
+    for (int i = tail - 1; i >= 0; --i) order[out++] = queue[i];   /* reversed component */
+  }
+  free(pairs); free(adj_off); free(adj); free(deg); free(key); free(vis); free(queue); free(nk);
+  return 0;
+}
+
+/* SplitMix64 finaliser (Steele, Lea & Flood 2014 / Vigna), the column hash
+ * of mix_column (CFE:251-256). */
+static uint64_t splitmix64(uint64_t v) {
+  v += 0x9e3779b97f4a7c15ULL;
+  v = (v ^ (v >> 30)) * 0xbf58476d1ce4e5b9ULL;
+  v = (v ^ (v >> 27)) * 0x94d049bb133111ebULL;
+  return v ^ (v >> 31);
+}
+
+/* row_jaccard (CFE:266-294): run-merge of the two rows' column lists in
+ * storage order, counting distinct runs; 1.0 when both are empty. */
+static double jaccard(int a, int b, const int *rowptr, const int *colind) {
+  int l = rowptr[a], r = rowptr[b];
+  const int le = rowptr[a + 1], re = rowptr[b + 1];
+  int inter = 0, lu = 0, ru = 0;
+  while (l < le || r < re) {
+    int lc = l < le ? colind[l] : 0x7fffffff;
+    int rc = r < re ? colind[r] : 0x7fffffff;
+    if (lc == rc) {
+      ++inter; ++lu; ++ru;
+      while (l < le && colind[l] == lc) ++l;
+      while (r < re && colind[r] == rc) ++r;
+    } else if (lc < rc) {
+      ++lu;
+      while (l < le && colind[l] == lc) ++l;
+    } else {
+      ++ru;
+      while (r < re && colind[r] == rc) ++r;
+    }
+  }
+  int un = lu + ru - inter;
+  return un ? (double)inter / un : 1.0;
+}
+
+typedef struct { uint64_t sig; int first; int row; } rank_t;
+static int cmp_rank(const void *a, const void *b) {
+  const rank_t *x = (const rank_t *)a, *y = (const rank_t *)b;
+  if (x->sig != y->sig) return x->sig < y->sig ? -1 : 1;
+  if (x->first != y->first) return x->first < y->first ? -1 : 1;
+  return (x->row > y->row) - (x->row < y->row);
+}
+
+/* jaccard_greedy_order (CFE:300-340): rows ranked by (minhash of columns,
+ * first column, row); buckets of 64 consecutive ranked rows; inside a
+ * bucket start from its first row and repeatedly append the remaining row
+ * of highest Jaccard similarity to the last appended row (ties: lower row
+ * id). */
+void oracle_order_jaccard(int m, int k, const int *rowptr, const int *colind, int *order) {
+  rank_t *rk = (rank_t *)malloc(sizeof(rank_t) * (size_t)(m > 0 ? m : 1));
+  for (int r = 0; r < m; ++r) {
+    uint64_t s = UINT64_MAX;
+    for (int p = rowptr[r]; p < rowptr[r + 1]; ++p) {
+      uint64_t h = splitmix64((uint64_t)(uint32_t)colind[p]);
+      if (h < s) s = h;
+    }
+    rk[r].sig = s; rk[r].first = first_col(r, k, rowptr, colind); rk[r].row = r;
+  }
+  qsort(rk, (size_t)m, sizeof(rank_t), cmp_rank);
+  int out = 0;
+  int rem[64];
+  for (int base = 0; base < m; base += 64) {
+    int end = base + 64 < m ? base + 64 : m;
+    int n = 0;
+    for (int i = base + 1; i < end; ++i) rem[n++] = rk[i].row;
+    int cur = rk[base].row;
+    order[out++] = cur;
+    while (n > 0) {
+      int best = 0;
+      double bs = -1.0;
+      for (int c = 0; c < n; ++c) {
+        double s = jaccard(cur, rem[c], rowptr, colind);
+        if (s > bs || (s == bs && rem[c] < rem[best])) { bs = s; best = c; }
+      }
+      cur = rem[best];
+      order[out++] = cur;
+      for (int c = best; c + 1 < n; ++c) rem[c] = rem[c + 1];
+      --n;
+    }
+  }
+  free(rk);
+}
+
+/* Non-empty rows in order (the sparse-row physicalisation, CFE:483-488).
+ * Returns the count. */
+int oracle_order_sparse_rows(int m, const int *rowptr, int *order) {
+  int n = 0;
+  for (int r = 0; r < m; ++r)
+    if (rowptr[r] != rowptr[r + 1]) order[n++] = r;
+  return n;
+}
+
+/* Generated-operator packing (CFE:496-640) for BH x BW tiles:
+ *   packing 0 = column-condensed dense (modes 2 and 4), 1 = active fixed
+ *   blocks dense (mode 3, tile columns 8j..8j+7 clamped to k-1);
+ *   duplicates are summed; rows follow order[0..P) (new -> original).
+ * count pass: fills soff[ceil(P/BH)+1], returns the tile count (or -1 on an
+ * out-of-range column). fill pass writes sidx[BW*tiles], val[BH*BW*tiles]. */
+static int64_t pack_window(const int *rowptr, const int *colind, const float *values,
+                           int k, int bh, int bw, int packing, const int *order, int P, int w,
+                           int64_t **buf, int64_t *cap, int *sidx, float *val) {
+  int64_t n = 0;
+  for (int nr = w * bh; nr < (w + 1) * bh && nr < P; ++nr) {
+    int orow = order[nr];
+    for (int p = rowptr[orow]; p < rowptr[orow + 1]; ++p) {
+      if (colind[p] < 0 || colind[p] >= k) return -1;
+      if (n >= *cap) { *cap = *cap < 256 ? 256 : *cap * 2; *buf = (int64_t *)realloc(*buf, sizeof(int64_t) * 2 * (size_t)*cap); }
+      (*buf)[2 * n] = packing == 0 ? colind[p] : colind[p] / bw;
+      (*buf)[2 * n + 1] = ((int64_t)(nr - w * bh) << 32) | (uint32_t)p;
+      ++n;
+    }
+  }
+  qsort(*buf, (size_t)n, 2 * sizeof(int64_t), cmp_key2);
+  /* distinct keys in order */
+  int64_t nk = 0;
+  for (int64_t i = 0; i < n; ++i)
+    if (i == 0 || (*buf)[2 * i] != (*buf)[2 * i - 2]) ++nk;
+  int64_t tiles = packing == 0 ? (nk + bw - 1) / bw : nk;
+  if (!sidx) return tiles;
+  int64_t key_idx = -1;
+  for (int64_t i = 0; i < n; ++i) {
+    if (i == 0 || (*buf)[2 * i] != (*buf)[2 * i - 2]) ++key_idx;
+    int64_t key = (*buf)[2 * i];
+    int lrow = (int)((*buf)[2 * i + 1] >> 32);
+    int p = (int)((*buf)[2 * i + 1] & 0xffffffff);
+    int64_t tile, lcol;
+    if (packing == 0) { tile = key_idx / bw; lcol = key_idx % bw; }
+    else { tile = key_idx; lcol = colind[p] % bw; }
+    (void)key;
+    val[tile * bh * bw + oracle_swizzle(lrow * bw + (int)lcol)] += values[p];
+  }
+  /* tile columns */
+  key_idx = -1;
+  for (int64_t i = 0; i < n; ++i) {
+    if (!(i == 0 || (*buf)[2 * i] != (*buf)[2 * i - 2])) continue;
+    ++key_idx;
+    int64_t key = (*buf)[2 * i];
+    if (packing == 0) sidx[key_idx] = (int)key;
+    else for (int c = 0; c < bw; ++c) { int64_t col = key * bw + c; sidx[key_idx * bw + c] = (int)(col < k - 1 ? col : k - 1); }
+  }
+  if (packing == 0 && nk % bw) {
+    int last = sidx[nk - 1];
+    for (int64_t i = nk; i < tiles * bw; ++i) sidx[i] = last;
+  }
+  return tiles;
+}
+
+int64_t oracle_pack_count(const int *rowptr, const int *colind, int k, int bh, int bw, int packing,
+                          const int *order, int P, int *soff) {
+  int W = (P + bh - 1) / bh;
+  int64_t *buf = NULL, cap = 0, total = 0;
+  for (int w = 0; w < W; ++w) {
+    soff[w] = (int)total;
+    int64_t t = pack_window(rowptr, colind, NULL, k, bh, bw, packing, order, P, w, &buf, &cap, NULL, NULL);
+    if (t < 0) { free(buf); return -1; }
+    total += t;
+  }
+  soff[W] = (int)total;
+  free(buf);
+  return total;
+}
+
+void oracle_pack_fill(const int *rowptr, const int *colind, const float *values, int k, int bh, int bw,
+                      int packing, const int *order, int P, const int *soff, int *sidx, float *val) {
+  int W = (P + bh - 1) / bh;
+  int64_t *buf = NULL, cap = 0;
+  memset(val, 0, sizeof(float) * (size_t)((int64_t)soff[W] * bh * bw));
+  for (int w = 0; w < W; ++w)
+    pack_window(rowptr, colind, values, k, bh, bw, packing, order, P, w, &buf, &cap,
+                sidx + (int64_t)soff[w] * bw, val + (int64_t)soff[w] * bh * bw);
+  free(buf);
+}

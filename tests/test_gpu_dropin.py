@@ -121,6 +121,52 @@ def test_run_errors(gpu, monkeypatch):
         S.plan_for(rwo).run(torch.ones((int(colind.max()), 64), device="cuda"))
 
 
+@pytest.mark.parametrize("packing", ["column_condensed_dense", "active_fixed_blocks_dense"])
+@pytest.mark.parametrize("order", ["row_rcm", "first_col_sort", "jaccard_greedy", "sparse_rows"])
+@pytest.mark.parametrize("blk", [(16, 8), (32, 32)])
+def test_packed_plans_match_oracle(gpu, packing, order, blk):
+    """Reordered / sparse-row / fixed-block plans with summed duplicates:
+    the inverse row map is applied in the store, omitted rows are zero."""
+    import torch
+    from mask_amd.SRBCRSSpMM import Plan
+    M = K = 300
+    N = 128
+    rowptr, colind, values = random_csr(M, K, 0.03, seed=len(order) + blk[0], duplicates=True, empty_rows=0.3,
+                                        heavy_rows=2, heavy_len=250)
+    B = np.random.default_rng(3).uniform(-1, 1, (K, N)).astype(np.float32)
+    _say("packed", packing, order, blk)
+    plan = Plan(*(torch.from_numpy(a).cuda() for a in (rowptr, colind, values)), M, blk[0], blk[1],
+                packing=packing, dup="sum", row_order=order, K=K)
+    dB = torch.from_numpy(B).cuda()
+    for pol in (("row", 0), ("split", 2), ("strict_lb", 7)):
+        plan.set_schedule(*pol)
+        out = torch.full((M, N), float("nan"), device="cuda")
+        plan.run(dB, out)
+        torch.cuda.synchronize()
+        assert_gate(gate(out.cpu().numpy(), rowptr, colind, values, B, M))   # duplicates summed
+
+
+def test_generated_operator_on_packed_plan(gpu):
+    import torch
+    from mask_amd.build import GENERATED
+    from mask_amd.emitter import GeneratedOperator
+    from mask_amd.SRBCRSSpMM import Plan
+    M = K = 400
+    rowptr, colind, values = random_csr(M, K, 0.02, seed=17, empty_rows=0.4)
+    B = np.random.default_rng(17).uniform(-1, 1, (K, 256)).astype(np.float32)
+    _say("generated packed", M)
+    plan = Plan(*(torch.from_numpy(a).cuda() for a in (rowptr, colind, values)), M, packing="column_condensed_dense",
+                dup="sum", row_order="sparse_rows", K=K)
+    op = GeneratedOperator(GENERATED / "sr_bcrs_16x8.so")
+    dB = torch.from_numpy(B).cuda()
+    for pol, param in (("row", 0), ("split", 2)):
+        plan.set_schedule(pol, param)
+        ref = plan.run(dB)
+        out = op.run(plan, dB, schedule=pol, schedule_param=param)
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), pol
+
+
 def test_32x32_knobs_and_schedules(gpu):
     import torch
     from mask_amd.SRBCRSSpMM import Plan

@@ -244,3 +244,61 @@ def test_csr_transpose_matches_dense():
         assert (np.diff(tci[trp[r]:trp[r + 1]]) > 0).all()
         At[r, tci[trp[r]:trp[r + 1]]] = tv[trp[r]:trp[r + 1]]
     assert np.array_equal(At, A.T)
+
+
+# ---- row orders and generated-operator packings (library vs oracle) --------------
+
+_ORDER_CASES = [
+    dict(m=300, k=300, density=0.02, seed=1),
+    dict(m=257, k=257, density=0.05, seed=2, unsorted=True, duplicates=True, empty_rows=0.2),
+    dict(m=1000, k=1000, density=0.004, seed=3, empty_rows=0.3, heavy_rows=3, heavy_len=300),
+]
+
+
+@pytest.mark.parametrize("method", ["row_rcm", "first_col_sort", "jaccard_greedy", "sparse_rows", "identity"])
+@pytest.mark.parametrize("case", range(len(_ORDER_CASES)))
+def test_row_orders_match_oracle(method, case):
+    c = dict(_ORDER_CASES[case])
+    m, k = c.pop("m"), c.pop("k")
+    rp, ci, _ = random_csr(m, k, c.pop("density"), c.pop("seed"), **c)
+    assert np.array_equal(_capi.row_order_host(rp, ci, m, k, method), oracle.row_order(rp, ci, m, k, method))
+
+
+def test_row_orders_on_workload_graph():
+    m = datasets.gcn_graph(n=4000, avg_degree=10)
+    for method in ("row_rcm", "first_col_sort", "jaccard_greedy"):
+        assert np.array_equal(_capi.row_order_host(m.rowptr, m.colind, m.M, m.K, method),
+                              oracle.row_order(m.rowptr, m.colind, m.M, m.K, method)), method
+
+
+@pytest.mark.parametrize("packing", ["column_condensed_dense", "active_fixed_blocks_dense"])
+@pytest.mark.parametrize("blk", [(16, 8), (32, 32)])
+@pytest.mark.parametrize("order_kind", ["identity", "row_rcm", "sparse_rows"])
+def test_packing_matches_oracle(packing, blk, order_kind):
+    m = k = 333
+    rp, ci, vv = random_csr(m, k, 0.03, seed=7, unsorted=True, duplicates=True, empty_rows=0.25)
+    order = oracle.row_order(rp, ci, m, k, order_kind)
+    a = _capi.pack_host(rp, ci, vv, m, k, order=None if order_kind == "identity" else order, blk_h=blk[0],
+                        blk_w=blk[1], packing=packing, dup="sum")
+    b = oracle.pack(rp, ci, vv, k, order, blk[0], blk[1], packing=0 if packing.startswith("column") else 1)
+    assert np.array_equal(a["soff"], b["soff"]) and np.array_equal(a["sidx"], b["sidx"])
+    assert a["val"].tobytes() == b["val"].tobytes()
+
+
+def test_packing_last_write_equals_canonical_conversion():
+    m, k = 200, 500
+    rp, ci, vv = random_csr(m, k, 0.04, seed=9, unsorted=True, duplicates=True)
+    a = _capi.pack_host(rp, ci, vv, m, k, dup="last")
+    b = oracle.convert(rp, ci, vv, m)
+    assert np.array_equal(a["soff"], b["soff"]) and np.array_equal(a["sidx"], b["sidx"])
+    assert a["val"].tobytes() == b["val"].tobytes()
+
+
+def test_packing_rejects_bad_options():
+    rp, ci, vv = random_csr(20, 30, 0.2, seed=1)
+    with pytest.raises(_capi.SrbcrsError, match="distinct rows"):
+        _capi.pack_host(rp, ci, vv, 20, 30, order=[0, 0, 1])
+    with pytest.raises(_capi.SrbcrsError, match="out of range"):
+        _capi.pack_host(rp, ci, vv, 20, 5)
+    with pytest.raises(_capi.SrbcrsError, match="square"):
+        _capi.row_order_host(rp, ci, 20, 30, "row_rcm")

@@ -254,6 +254,130 @@ def test_segment_auto_hand_cases():
     assert s["cap"] == 2 and s["seg_end"].tolist() == [2, 3, 5, 7, 8, 10]
 
 
+def _csr_from_rows(rows, m):
+    rp, ci, vv = [0], [], []
+    for r in range(m):
+        for c, v in rows.get(r, []):
+            ci.append(c)
+            vv.append(v)
+        rp.append(len(ci))
+    return np.array(rp, np.int32), np.array(ci, np.int32), np.array(vv, np.float32)
+
+
+def test_first_col_order_hand_case():
+    rp, ci, _ = _csr_from_rows({0: [(5, 1.0)], 1: [(7, 1.0), (2, 1.0)], 3: [(2, 1.0)], 4: [(0, 1.0)]}, 5)
+    assert oracle.row_order(rp, ci, 5, 9, "first_col_sort").tolist() == [4, 1, 3, 0, 2]
+
+
+def test_rcm_hand_cases():
+    # path 0-1-2-3: start at the lowest-degree, lowest-id end, BFS, reverse
+    rp, ci, _ = _csr_from_rows({0: [(1, 1.0)], 1: [(2, 1.0)], 2: [(3, 1.0)]}, 4)
+    assert oracle.row_order(rp, ci, 4, 4, "row_rcm").tolist() == [3, 2, 1, 0]
+    # star centre 0 with leaves 1..3 and an isolated 4 (degree 0 starts first)
+    rp, ci, _ = _csr_from_rows({0: [(1, 1.0), (2, 1.0), (3, 1.0), (0, 1.0)]}, 5)
+    assert oracle.row_order(rp, ci, 5, 5, "row_rcm").tolist() == [4, 3, 2, 0, 1]
+    with pytest.raises(ValueError, match="square"):
+        oracle.row_order(rp, ci, 5, 6, "row_rcm")
+
+
+def test_rcm_recovers_band_structure():
+    """A banded matrix under a random symmetric permutation: RCM brings the
+    bandwidth back near the original (a plausible ordering bug would not)."""
+    n, bw = 400, 3
+    rng = np.random.default_rng(0)
+    perm = rng.permutation(n)
+    inv = np.argsort(perm)
+    rows = {}
+    for i in range(n):
+        for j in range(max(0, i - bw), min(n, i + bw + 1)):
+            rows.setdefault(int(inv[i]), []).append((int(inv[j]), 1.0))
+    rp, ci, _ = _csr_from_rows({r: sorted(v) for r, v in rows.items()}, n)
+    order = oracle.row_order(rp, ci, n, n, "row_rcm")
+    assert sorted(order.tolist()) == list(range(n))
+    pos = np.empty(n, np.int64)
+    pos[order] = np.arange(n)
+    band = max(abs(pos[r] - pos[c]) for r in range(n) for c in ci[rp[r]:rp[r + 1]])
+    scrambled = max(abs(r - c) for r in range(n) for c in ci[rp[r]:rp[r + 1]])
+    assert band <= 2 * bw and scrambled > 50
+
+
+def _splitmix64(v):
+    M = (1 << 64) - 1
+    v = (v + 0x9E3779B97F4A7C15) & M
+    v = ((v ^ (v >> 30)) * 0xBF58476D1CE4E5B9) & M
+    v = ((v ^ (v >> 27)) * 0x94D049BB133111EB) & M
+    return v ^ (v >> 31)
+
+
+def _jaccard_greedy_py(rp, ci, m, k):
+    """Brute-force restatement from the description (minhash buckets of 64,
+    greedy nearest Jaccard on column sets, ties to the lower row id)."""
+    sets = [list(ci[rp[r]:rp[r + 1]]) for r in range(m)]
+    sig = [min((_splitmix64(int(c) & 0xFFFFFFFF) for c in s), default=(1 << 64) - 1) for s in sets]
+    first = [min((int(c) for c in s if 0 <= c < k), default=k) for s in sets]
+    ranked = sorted(range(m), key=lambda r: (sig[r], first[r], r))
+    out = []
+    for b in range(0, m, 64):
+        bucket = ranked[b:b + 64]
+        cur, rem = bucket[0], bucket[1:]
+        out.append(cur)
+        while rem:
+            def jac(a, c):
+                A, C = set(sets[a]), set(sets[c])
+                return len(A & C) / len(A | C) if (A | C) else 1.0
+            best = max(rem, key=lambda c: (jac(cur, c), -c))
+            rem.remove(best)
+            out.append(best)
+            cur = best
+    return out
+
+
+def test_splitmix64_reference_vector():
+    # first output of SplitMix64 seeded with 0 (Vigna's reference generator)
+    assert _splitmix64(0) == 0xE220A8397B1DCDAF
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_jaccard_greedy_matches_bruteforce(seed):
+    m, k = 150, 60
+    rp, ci, _ = random_csr(m, k, 0.08, seed, empty_rows=0.1)     # sorted rows: the merge walk is exact
+    assert oracle.row_order(rp, ci, m, k, "jaccard_greedy").tolist() == _jaccard_greedy_py(rp, ci, m, k)
+
+
+def test_sparse_rows_order():
+    rp, ci, _ = _csr_from_rows({1: [(0, 1.0)], 3: [(2, 1.0)]}, 5)
+    assert oracle.row_order(rp, ci, 5, 3, "sparse_rows").tolist() == [1, 3]
+
+
+def test_pack_hand_cases():
+    # r0: col 3 twice (summed), r1: col 9; rows reordered [1, 0]
+    rp, ci, vv = _csr_from_rows({0: [(3, 1.0), (3, 2.0)], 1: [(9, 4.0)]}, 2)
+    p = oracle.pack(rp, ci, vv, 10, [1, 0])
+    assert p["soff"].tolist() == [0, 1]
+    assert p["sidx"].tolist() == [3, 9, 9, 9, 9, 9, 9, 9]
+    val = np.zeros(128, np.float32)
+    val[1] = 4.0          # new row 0 (old row 1), condensed col 1
+    val[8] = 3.0          # new row 1 (old row 0), condensed col 0, 1 + 2 summed
+    assert p["val"].tobytes() == val.tobytes()
+    f = oracle.pack(rp, ci, vv, 10, [1, 0], packing=1)
+    assert f["sidx"].tolist() == list(range(8)) + [8, 9, 9, 9, 9, 9, 9, 9]   # clamped to k - 1
+    val = np.zeros(256, np.float32)
+    val[11] = 3.0         # block 0: new row 1, col 3
+    val[128 + 1] = 4.0    # block 1: new row 0, col 9 -> local 1
+    assert f["val"].tobytes() == val.tobytes()
+    with pytest.raises(ValueError, match="out of range"):
+        oracle.pack(rp, ci, vv, 9, [0, 1])
+
+
+def test_pack_identity_equals_canonical_conversion():
+    m, k = 97, 300
+    rp, ci, vv = random_csr(m, k, 0.05, seed=4, unsorted=True)
+    a = oracle.pack(rp, ci, vv, k, np.arange(m))
+    b = oracle.convert(rp, ci, vv, m)
+    assert np.array_equal(a["soff"], b["soff"]) and np.array_equal(a["sidx"], b["sidx"])
+    assert a["val"].tobytes() == b["val"].tobytes()
+
+
 def test_segment_reduce_matches_numpy():
     rng = np.random.default_rng(0)
     wso = np.array([0, 2, 2, 5], np.int32)
