@@ -27,19 +27,44 @@ def test_select_backend_sr_bcrs():
 
 @pytest.mark.parametrize("mutate,msg", [
     (lambda s: s.update(atomic={"type": "mco", "x_axis": "X_i", "y_axis": "Y_si"}), "dense atomic"),
-    (lambda s: s["levels"].pop(), "two-level"),
+    (lambda s: s["levels"].pop(), "requires axis Y_o_s"),
     (lambda s: s["levels"][0]["axes"][1].update(type="df"), "axis Y_s"),
     (lambda s: s["atomic"].update(y_axis="Y_so"), "x_axis=X_i and y_axis=Y_si"),
     (lambda s: s["atomic"].update(layout="col_major"), "row-major"),
     (lambda s: s["params"].update(BLK_M=8), "BLK_M x BLK_K"),
     (lambda s: s["params"].pop("BLK_K"), "concrete integer"),
-    (lambda s: s["levels"][0]["axes"][0].update(reorder="row_rcm"), "reorders"),
+    (lambda s: s["levels"][0]["axes"][0].update(reorder="random"), "reorder contract"),
+    (lambda s: s["levels"][0]["axes"][1].update(reorder="row_rcm"), "outer sparse/dense row axis"),
+    (lambda s: s["levels"].extend([s["levels"][0], s["levels"][1]]), "hierarchy"),
+    (lambda s: s["levels"].append(s["levels"][0]), "requires axis X_s"),
 ])
 def test_select_backend_rejects(mutate, msg):
     spec = copy.deepcopy(sr_bcrs_spec())
     mutate(spec)
     with pytest.raises(ValueError, match=msg):
         select_backend(spec)
+
+
+def test_select_backend_other_sr_bcrs_hierarchies():
+    from mask_amd.backend_registry import fixed_block_spec, plan_options, sparse_row_spec
+    fb = select_backend(fixed_block_spec())
+    assert (fb.packing_mode, fb.codegen_format_name) == ("active_fixed_blocks_dense", "SR_BCRS")
+    assert plan_options(fb)["packing"] == "active_fixed_blocks_dense"
+    sr = select_backend(sparse_row_spec(32, 32))
+    assert sr.packing_mode == "sparse_row_column_condensed_dense" and sr.physical_blk_m == 32
+    assert plan_options(sr)["row_order"] == "sparse_rows" and plan_options(sr)["dup"] == "sum"
+    spec = sr_bcrs_spec()
+    spec["levels"][0]["axes"][0]["reorder"] = "jaccard_greedy"
+    p = select_backend(spec)
+    assert p.row_reorder == "jaccard_greedy" and plan_options(p)["row_order"] == "jaccard_greedy"
+    bad = sparse_row_spec()
+    bad["levels"][0]["axes"][0]["reorder"] = "row_rcm"
+    with pytest.raises(ValueError, match="does not yet compose"):
+        select_backend(bad)
+    bad = fixed_block_spec()
+    bad["atomic"]["y_axis"] = "Y_o_s"
+    with pytest.raises(ValueError, match="y_axis=Y_i"):
+        select_backend(bad)
 
 
 def test_select_backend_targets_and_tiles():
