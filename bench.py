@@ -34,6 +34,7 @@ def parse():
     ap.add_argument("--config", default="uniform-65536",
                     choices=["uniform-4096", "uniform-65536", "banded-524288", "rmat-2^20", "gcn-232965"])
     ap.add_argument("--N", type=int, default=None, help="dense width (default: the workload's)")
+    ap.add_argument("--mtx", default=None, help="a MatrixMarket file instead of a synthetic workload")
     ap.add_argument("--schedule", default="auto", help="row | split[:cap] | strict_lb[:w] | multi_bind | auto")
     ap.add_argument("--kernel", default="srbcrs", choices=["srbcrs", "csr"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline leg")
@@ -88,7 +89,7 @@ def main():
 
     dev = torch.device("cuda", 0)
     t0 = time.time()
-    m = datasets.make_config(args.config)
+    m = datasets.from_mtx(args.mtx, N=args.N or 512) if args.mtx else datasets.make_config(args.config)
     N = args.N or m.N
     B_host = m.dense(N)
     print(f"[bench] workload {m.name} M={m.M} K={m.K} nnz={m.nnz} N={N} gen {time.time() - t0:.1f}s",

@@ -200,6 +200,14 @@ def gcn_graph(n: int = 232965, avg_degree: int = 50, N: int = 256, seed: int = C
                       dense_dist="normal")
 
 
+def from_mtx(path, N: int = 512, seed: int = 7) -> CSRMatrix:
+    """A MatrixMarket file as a workload (the reference's dataset path,
+    examples/src/mmio_highlevel.cu:255-402); dense operand U[-1, 1]."""
+    from .mtx import read_mtx
+    m, n, rowptr, colind, values, sym = read_mtx(path)
+    return CSRMatrix(str(path), rowptr, colind, values, m, n, N, "uniform", seed, dict(symmetric=sym))
+
+
 def make_config(name: str, scale_down: int = 1) -> CSRMatrix:
     """The named workload.  scale_down > 1 shrinks M/K (and edge counts) by
     that factor for quick tests while keeping the structure."""

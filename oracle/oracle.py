@@ -251,6 +251,42 @@ def pack(rowptr, colind, values, k: int, order, blk_h: int = 16, blk_w: int = 8,
     return dict(soff=soff, sidx=sidx[: total * blk_w], val=val[: total * blk_h * blk_w], total=total)
 
 
+def read_mtx_loop(path):
+    """Loop restatement of mmio_allinone (examples/src/mmio_highlevel.cu:
+    255-402): per-row counters, exclusive scan, then entries placed in file
+    order; symmetric/hermitian off-diagonals also placed mirrored right after.
+    Small files only."""
+    lines = [l for l in open(path).read().splitlines()]
+    banner = lines[0].split()
+    field, sym = banner[3].lower(), banner[4].lower()
+    body = [l for l in lines[1:] if l.strip() and not l.lstrip().startswith("%")]
+    m, n, nnz = (int(x) for x in body[0].split()[:3])
+    ri, ci, vv = [], [], []
+    for l in body[1:1 + nnz]:
+        t = l.split()
+        ri.append(int(t[0]) - 1)
+        ci.append(int(t[1]) - 1)
+        vv.append(1.0 if field == "pattern" else float(int(t[2])) if field == "integer" else float(t[2]))
+    symmetric = sym in ("symmetric", "hermitian")
+    count = [0] * (m + 1)
+    for i in range(nnz):
+        count[ri[i]] += 1
+        if symmetric and ri[i] != ci[i]:
+            count[ci[i]] += 1
+    start = [0] * (m + 1)
+    for r in range(m):
+        start[r + 1] = start[r] + count[r]
+    fill = [0] * m
+    col = [0] * start[m]
+    val = [0.0] * start[m]
+    for i in range(nnz):
+        for r, c in ((ri[i], ci[i]), (ci[i], ri[i])) if symmetric and ri[i] != ci[i] else ((ri[i], ci[i]),):
+            col[start[r] + fill[r]] = c
+            val[start[r] + fill[r]] = vv[i]
+            fill[r] += 1
+    return m, n, np.array(start, np.int32), np.array(col, np.int32), np.array(val, np.float32), symmetric
+
+
 def error_metrics(C, C64, absAB):
     """Gate metrics.  North star: |C - C64| <= 1e-4 * (|A||B|) elementwise and
     a relative-L2 bound; the reference's own gate |d| <= 1e-3 + 1e-3*|ref|
