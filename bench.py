@@ -35,6 +35,11 @@ def parse():
                     choices=["uniform-4096", "uniform-65536", "banded-524288", "rmat-2^20", "gcn-232965"])
     ap.add_argument("--N", type=int, default=None, help="dense width (default: the workload's)")
     ap.add_argument("--mtx", default=None, help="a MatrixMarket file instead of a synthetic workload")
+    ap.add_argument("--gcn-forward", action="store_true",
+                    help="time the GCN workload's two-layer forward instead of one SpMM")
+    ap.add_argument("--row-order", default="identity",
+                    choices=["identity", "row_rcm", "first_col_sort", "jaccard_greedy"],
+                    help="pack rows in this order (inverse map fused into the kernel store)")
     ap.add_argument("--schedule", default="auto", help="row | split[:cap] | strict_lb[:w] | multi_bind | auto")
     ap.add_argument("--kernel", default="srbcrs", choices=["srbcrs", "csr"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline leg")
@@ -63,6 +68,64 @@ def copy_calibration(mib):
     print(json.dumps({"copy_calibration_bytes_read": n * 4, "copy_calibration_bytes_written": n * 4}))
 
 
+def gcn_forward_bench(args):
+    """The GCN workload's two-layer forward relu(A (X W1)) -> A (H W2) on
+    one GPU: SpMM at N = 256 and N = 64 (SR-BCRS 16x8, split schedule) plus
+    the dense GEMMs (torch / hipBLASLt).  One JSON line."""
+    import torch
+    from mask_amd import datasets
+    from mask_amd.gcn import glorot_weights
+    from mask_amd.SRBCRSSpMM import Plan
+    dev = torch.device("cuda", 0)
+    m = datasets.make_config("gcn-232965")
+    gen = torch.Generator(device="cpu")
+    gen.manual_seed(m.seed)
+    X = torch.randn((m.M, 512), generator=gen).to(dev)
+    w1, w2 = glorot_weights([512, 256, 64], seed=m.seed, device=dev)
+    t = lambda a: torch.from_numpy(a).to(dev)
+    plan = Plan(t(m.rowptr), t(m.colind), t(m.values), m.M)
+    plan.set_schedule("split", 0)
+    h1 = torch.empty((m.M, 256), device=dev)
+    out = torch.empty((m.M, 64), device=dev)
+
+    def fwd():
+        plan.run(X @ w1, h1)
+        torch.relu_(h1)
+        plan.run(h1 @ w2, out)
+
+    for _ in range(args.warmup):
+        fwd()
+    torch.cuda.synchronize()
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    e[0].record()
+    for _ in range(args.steps):
+        fwd()
+    e[1].record()
+    torch.cuda.synchronize()
+    ms = e[0].elapsed_time(e[1]) / args.steps
+    # SpMM share
+    xw, hw = X @ w1, h1 @ w2
+    s = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    torch.cuda.synchronize()
+    s[0].record()
+    for _ in range(args.steps):
+        plan.run(xw, h1)
+    s[1].record()
+    for _ in range(args.steps):
+        plan.run(hw, out)
+    s[2].record()
+    torch.cuda.synchronize()
+    sp256, sp64 = s[0].elapsed_time(s[1]) / args.steps, s[1].elapsed_time(s[2]) / args.steps
+    print(json.dumps({
+        "metric": "GCN two-layer forward time (gcn-232965, features 512, hidden 256, out 64)",
+        "value": round(ms, 4), "unit": "ms", "higher_is_better": False, "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "dtype": "f32", "data": "synthetic R-MAT graph + N(0,1) features (seeded)",
+        "config": {"workload": m.name, "nodes": m.M, "nnz": m.nnz, "schedule": "split:auto"},
+        "spmm_ms": {"N256": round(sp256, 4), "N64": round(sp64, 4)},
+        "spmm_gflops": {"N256": round(2 * m.nnz * 256 / sp256 / 1e6, 1), "N64": round(2 * m.nnz * 64 / sp64 / 1e6, 1)},
+    }), flush=True)
+
+
 def algorithmic_bytes(M, N, Mo, nb, nnz, kernel):
     """Dataflow bytes per launch.  SR-BCRS: metadata + A blocks + B rows
     gathered per block + C written.  CSR: rowptr + (col, val) + B row per
@@ -81,6 +144,9 @@ def main():
 
     if args.copy_calibration_mb:
         copy_calibration(args.copy_calibration_mb)
+        return
+    if args.gcn_forward:
+        gcn_forward_bench(args)
         return
 
     import torch
@@ -102,7 +168,7 @@ def main():
     C = torch.empty((m.M, N), dtype=torch.float32, device=dev)
 
     t0 = time.time()
-    plan = Plan(rowptr_d, colind_d, values_d, m.M)
+    plan = Plan(rowptr_d, colind_d, values_d, m.M, row_order=args.row_order, K=m.K)
     conv_s = time.time() - t0
     nb, Mo = plan.total_blocks, plan.row_windows
     sched = args.schedule
@@ -161,7 +227,7 @@ def main():
         "data": "synthetic (seeded numpy, see mask_amd/datasets.py)",
         "config": {"workload": m.name, "M": m.M, "K": m.K, "N": N, "nnz": m.nnz, "blocks": nb,
                    "block_fill": round(m.nnz / (128 * max(nb, 1)), 4), "kernel": args.kernel,
-                   "schedule": f"{plan.policy[0]}:{plan.policy[1]}", "seed": m.seed,
+                   "schedule": f"{plan.policy[0]}:{plan.policy[1]}", "seed": m.seed, "row_order": args.row_order,
                    "conversion_s": round(conv_s, 3), "meta": m.meta,
                    "knobs": {"depth": args.depth or 2, "tile_b": args.tile_b, "wg_cols": args.wg_cols or 128,
                              "grid_order": args.grid_order or 1, "windows_per_wave": args.wpw or 1}},
@@ -169,7 +235,8 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(m.name, N, args.kernel,
                                                  not (args.depth or args.tile_b or args.wg_cols or args.grid_order
-                                                      or args.wpw) and args.schedule == "auto"),
+                                                      or args.wpw) and args.schedule == "auto"
+                                                 and args.row_order == "identity" and not args.mtx),
                      "algorithmic_bytes": int(ab), "compulsory_bytes": int(compulsory),
                      "compulsory_frac": round(compulsory / t_s / 1e9 / HBM_PEAK_GBS, 4),
                      "mfma_padded_tflops": round(padded_flops / t_s / 1e12, 3),
