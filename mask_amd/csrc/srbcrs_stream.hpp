@@ -226,6 +226,11 @@ __device__ __forceinline__ void flush_task(const Src& src, int t, f4 (&acc)[BH /
 // ring without draining it at task boundaries: the accumulator tile is
 // flushed and cleared when the unit index crosses a task's end.  Every
 // output element has exactly one writer per launch: no atomics.
+//
+// Occupancy is left to the compiler: forcing 4 waves/SIMD on the default
+// instantiation (amdgpu_waves_per_eu, 98 registers instead of 146) made it
+// slower on the GPU (GCN N=256 1.83 -> 2.02 ms), because the tighter budget
+// delays the ring's loads.
 template <class Src, int BH, int BW, int VEC, int G, int WAVES, int DEPTH>
 __global__ __launch_bounds__(64 * WAVES) void spmm_stream(
     Src src, const float* __restrict__ B, float* __restrict__ C, float* __restrict__ partial,
