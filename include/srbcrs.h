@@ -54,10 +54,12 @@ int srbcrs_convert_fill(const int32_t *rowptr, const int32_t *colind, const floa
 /* ---- Plans: the device-resident SR-BCRS matrix.  Replaces the reference's
  * preprocess_gpu_srcfp32_srbcrs + its process-global CacheEntry
  * (SRK:27-45, SRK:172-393; pybind preprocess_gpu_16x8 / preprocess_gpu at
- * SRC:77-118).  Inputs are CSR arrays on the device (is_device = 1, copied
- * to the host for conversion as the reference does) or on the host.  On
- * success *out owns device copies of soff / sidx / val on the current
- * device. */
+ * SRC:77-118).  is_device: 0 = the CSR arrays are on the host; 1 = on the
+ * device, converted on the device (radix sort of (window, column) keys, no
+ * host round trip); 2 = on the device, copied to the host and converted
+ * there as the reference does (SRK:203-205).  All three give the same
+ * arrays bit for bit.  On success *out owns device copies of soff / sidx /
+ * val on the current device. */
 int srbcrs_plan_create(const int32_t *rowptr, const int32_t *colind, const float *values,
                        int32_t num_nodes, int64_t nnz, int32_t blk_h, int32_t blk_w,
                        int32_t is_device, void *stream, srbcrs_plan **out);

@@ -43,7 +43,7 @@ class Plan:
 
     def __init__(self, rowptr, colind, values, num_nodes: int, blk_h: int = 16, blk_w: int = 8,
                  device: Optional[torch.device] = None, packing: str = "column_condensed_dense",
-                 dup: str = "last", row_order="identity", K: Optional[int] = None):
+                 dup: str = "last", row_order="identity", K: Optional[int] = None, convert_on: str = "device"):
         """CSR (device tensors, or host arrays) -> device-resident plan.
 
         The defaults are the reference's preprocess_gpu conversion.  The
@@ -51,7 +51,11 @@ class Plan:
         / "active_fixed_blocks_dense"), ``dup`` ("last" / "sum"),
         ``row_order`` ("identity", "row_rcm", "first_col_sort",
         "jaccard_greedy", "sparse_rows", or an explicit new -> original
-        sequence) and the column count ``K`` (required for fixed blocks)."""
+        sequence) and the column count ``K`` (required for fixed blocks).
+        ``convert_on`` ("device" / "host") picks where a device CSR is
+        converted for the canonical packing; the arrays are identical."""
+        if convert_on not in ("device", "host"):
+            raise ValueError("convert_on must be 'device' or 'host'")
         L = _capi.lib()
         on_dev = isinstance(rowptr, Tensor) and rowptr.is_cuda
         if on_dev:
@@ -76,7 +80,8 @@ class Plan:
         with torch.cuda.device(self.device):
             stream = _stream_handle(self.device) if on_dev else None
             _capi.check(L.srbcrs_plan_create_ex(_capi.ptr(rowptr), _capi.ptr(colind), _capi.ptr(values),
-                                                int(num_nodes), nnz, ctypes.byref(opts), 1 if on_dev else 0, stream,
+                                                int(num_nodes), nnz, ctypes.byref(opts),
+                                                (1 if convert_on == "device" else 2) if on_dev else 0, stream,
                                                 ctypes.byref(h)))
         self._h = h
         d = _capi.PlanDesc()

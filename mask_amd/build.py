@@ -62,7 +62,7 @@ def build(verbose: bool = False) -> Path:
 
     with ThreadPoolExecutor(max_workers=4) as ex:
         gen = [ex.submit(build_generated_one, bm, bk) for bm, bk in GENERATED_SHAPES]
-        objs = list(ex.map(compile_obj, ("srbcrs_kernels.hip", "srbcrs_capi.cpp", "srbcrs_pack.cpp")))
+        objs = list(ex.map(compile_obj, ("srbcrs_kernels.hip", "srbcrs_capi.cpp", "srbcrs_pack.cpp", "srbcrs_convert.hip")))
         for f in gen:
             f.result()
     tmp = LIB.with_suffix(".so.tmp")

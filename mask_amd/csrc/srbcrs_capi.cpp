@@ -16,6 +16,7 @@
 
 #include "../../include/srbcrs.h"
 #include "srbcrs_kernels.h"
+#include "srbcrs_convert.h"
 #include "srbcrs_pack.h"
 
 namespace {
@@ -412,6 +413,8 @@ struct srbcrs_plan {
   int32_t* d_rowmap = nullptr;
   int32_t* d_zero_rows = nullptr;
   int32_t n_zero_rows = 0;
+  // edge maps of a plan converted on the device (host vectors above are empty then)
+  int32_t *d_e2r = nullptr, *d_e2c = nullptr, *d_bp = nullptr;
 
   void free_schedule() {
     dev_free(d_group_off);
@@ -433,6 +436,9 @@ struct srbcrs_plan {
     dev_free(d_val);
     dev_free(d_rowmap);
     dev_free(d_zero_rows);
+    dev_free(d_e2r);
+    dev_free(d_e2c);
+    dev_free(d_bp);
     if (switched) (void)hipSetDevice(cur);
   }
 };
@@ -541,6 +547,49 @@ void create_packed(srbcrs_plan& plan, const int32_t* rp, const int32_t* ci, cons
   plan.sched.policy = "row";
 }
 
+void* conv_alloc(void*, size_t bytes) {
+  void* p = nullptr;
+  if (hipMalloc(&p, bytes) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  return p;
+}
+
+void conv_free(void*, void* p) { (void)hipFree(p); }
+
+// Canonical conversion of a device CSR on the device (srbcrs_convert.hip).
+void create_on_device(srbcrs_plan& plan, const int32_t* rowptr, const int32_t* colind,
+                      const float* values, hipStream_t st) {
+  const int32_t Mo = (plan.num_nodes + plan.blk_h - 1) / plan.blk_h;
+  plan.Mo = Mo;
+  plan.d_soff = dev_alloc<int32_t>((size_t)Mo + 1);
+  plan.d_e2r = dev_alloc<int32_t>((size_t)plan.nnz);
+  plan.d_e2c = dev_alloc<int32_t>((size_t)plan.nnz);
+  plan.d_bp = dev_alloc<int32_t>((size_t)Mo);
+  if (plan.nnz) {
+    hip_check(hipMemsetAsync(plan.d_e2r, 0, (size_t)plan.nnz * 4, st), "hipMemsetAsync");
+    hip_check(hipMemsetAsync(plan.d_e2c, 0, (size_t)plan.nnz * 4, st), "hipMemsetAsync");
+  }
+  srbcrs::DeviceConvertIn in{rowptr, colind, values, plan.num_nodes, plan.nnz, plan.blk_h, plan.blk_w,
+                             plan.d_e2r, plan.d_e2c, plan.d_bp};
+  srbcrs::DeviceConvertOut out;
+  out.soff = plan.d_soff;
+  const hipError_t e = srbcrs::device_convert(in, out, conv_alloc, conv_free, nullptr, st);
+  plan.d_sidx = out.sidx;   // owned by the plan from here on, even on failure
+  plan.d_val = out.val;
+  hip_check(e, "device conversion");
+  if (out.bad == 1) fail(SRBCRS_EINVAL, "rowptr must be non-decreasing and within [0, nnz]");
+  if (out.bad == 2) fail(SRBCRS_EINVAL, "colind holds a negative column index");
+  plan.total = out.total;
+  plan.max_col = out.max_col;
+  plan.h_soff.resize((size_t)Mo + 1);
+  hip_check(hipMemcpyAsync(plan.h_soff.data(), plan.d_soff, plan.h_soff.size() * 4, hipMemcpyDeviceToHost, st),
+            "copy soff");
+  hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
+  plan.sched.policy = "row";
+}
+
 }  // namespace
 
 extern "C" {
@@ -612,11 +661,27 @@ int srbcrs_plan_create_ex(const int32_t* rowptr, const int32_t* colind, const fl
                            o.row_order == SRBCRS_ORDER_IDENTITY;
     if (num_nodes < 1) fail(SRBCRS_EINVAL, "num_nodes must be positive");
     if (nnz < 0 || nnz > INT32_MAX) fail(SRBCRS_EINVAL, "nnz out of range");
+    if (is_device < 0 || is_device > 2) fail(SRBCRS_EINVAL, "is_device must be 0, 1 or 2");
     std::vector<int32_t> h_rowptr, h_colind;
     std::vector<float> h_values;
     const int32_t *rp = rowptr, *ci = colind;
     const float* vv = values;
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (canonical && is_device == 1) {
+      // device CSR converted in HBM (no host round trip)
+      if (!rowptr || (nnz > 0 && (!colind || !values))) fail(SRBCRS_EINVAL, "NULL CSR array");
+      auto plan = std::make_unique<srbcrs_plan>();
+      hip_check(hipGetDevice(&plan->device), "hipGetDevice");
+      plan->num_nodes = num_nodes;
+      plan->blk_h = blk_h;
+      plan->blk_w = blk_w;
+      plan->nnz = nnz;
+      plan->canonical = true;
+      plan->packed_rows = num_nodes;
+      create_on_device(*plan, rowptr, colind, values, st);
+      *out = plan.release();
+      return;
+    }
     if (is_device) {
       // the reference copies the device CSR to the host for conversion
       // (SRBCRSSpMM_kernel.cu:203-205)
@@ -762,6 +827,19 @@ int srbcrs_plan_write_edges(const srbcrs_plan* plan, int32_t* d_block_partition,
     if (!plan) fail(SRBCRS_EINVAL, "plan is NULL");
     if (!plan->canonical) fail(SRBCRS_EINVAL, "edge maps exist only for canonical (preprocess_gpu) plans");
     hipStream_t st = static_cast<hipStream_t>(stream);
+    if (plan->d_e2r) {   // converted on the device: device-to-device copies
+      if (d_block_partition && block_partition_len >= plan->Mo && plan->Mo > 0)
+        hip_check(hipMemcpyAsync(d_block_partition, plan->d_bp, (size_t)plan->Mo * 4, hipMemcpyDeviceToDevice, st),
+                  "copy block_partition");
+      if (d_edge_to_col && edge_to_col_len >= plan->nnz && plan->nnz > 0)
+        hip_check(hipMemcpyAsync(d_edge_to_col, plan->d_e2c, (size_t)plan->nnz * 4, hipMemcpyDeviceToDevice, st),
+                  "copy edge_to_col");
+      if (d_edge_to_row && edge_to_row_len >= plan->nnz && plan->nnz > 0)
+        hip_check(hipMemcpyAsync(d_edge_to_row, plan->d_e2r, (size_t)plan->nnz * 4, hipMemcpyDeviceToDevice, st),
+                  "copy edge_to_row");
+      hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
+      return;
+    }
     if (d_block_partition && block_partition_len >= plan->Mo && plan->Mo > 0)
       hip_check(hipMemcpyAsync(d_block_partition, plan->h_block_partition.data(), (size_t)plan->Mo * 4,
                                hipMemcpyHostToDevice, st), "copy block_partition");
