@@ -50,6 +50,8 @@ def parse():
     ap.add_argument("--wg-cols", type=int, default=0, help="kernel knob: columns per workgroup")
     ap.add_argument("--grid-order", type=int, default=0, help="kernel knob: 1 chunk-major, 2 window-major")
     ap.add_argument("--wpw", type=int, default=0, help="kernel knob: row windows streamed per wave")
+    ap.add_argument("--a-operand", default="default", choices=["default", "compact", "dense"],
+                    help="block-value copy the kernel reads (default: compact when blocks are at most half full)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="only run an elementwise copy of this many MiB (5 launches) to calibrate "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE against a known byte count")
@@ -126,6 +128,15 @@ def gcn_forward_bench(args):
     }), flush=True)
 
 
+def a_operand_used(plan, requested):
+    """The block-value copy the SR-BCRS kernel reads (mirrors the library's
+    default: compact when at most half of the block positions are stored)."""
+    if requested != "default":
+        return requested
+    stored = plan.desc.stored_values
+    return "compact" if stored >= 0 and 2 * stored <= plan.total_blocks * plan.blk_h * plan.blk_w else "dense"
+
+
 def algorithmic_bytes(M, N, Mo, nb, nnz, kernel):
     """Dataflow bytes per launch.  SR-BCRS: metadata + A blocks + B rows
     gathered per block + C written.  CSR: rowptr + (col, val) + B row per
@@ -181,7 +192,7 @@ def main():
 
     if args.kernel == "srbcrs":
         step = lambda: plan.run(B, C, depth=args.depth, tile_b=args.tile_b, wg_cols=args.wg_cols,
-                                grid_order=args.grid_order, windows_per_wave=args.wpw)
+                                grid_order=args.grid_order, windows_per_wave=args.wpw, a_operand=args.a_operand)
     else:
         step = lambda: csr_spmm(rowptr_d, colind_d, values_d, B, m.M, max_col=max_col, out=C)
 
@@ -230,12 +241,14 @@ def main():
                    "schedule": f"{plan.policy[0]}:{plan.policy[1]}", "seed": m.seed, "row_order": args.row_order,
                    "conversion_s": round(conv_s, 3), "meta": m.meta,
                    "knobs": {"depth": args.depth or 2, "tile_b": args.tile_b, "wg_cols": args.wg_cols or 128,
-                             "grid_order": args.grid_order or 1, "windows_per_wave": args.wpw or 1}},
+                             "grid_order": args.grid_order or 1, "windows_per_wave": args.wpw or 1,
+                             "a_operand": a_operand_used(plan, args.a_operand)}},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(m.name, N, args.kernel,
                                                  not (args.depth or args.tile_b or args.wg_cols or args.grid_order
                                                       or args.wpw) and args.schedule == "auto"
+                                                 and args.a_operand == "default"
                                                  and args.row_order == "identity" and not args.mtx),
                      "algorithmic_bytes": int(ab), "compulsory_bytes": int(compulsory),
                      "compulsory_frac": round(compulsory / t_s / 1e9 / HBM_PEAK_GBS, 4),

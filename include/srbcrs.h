@@ -81,6 +81,7 @@ typedef struct srbcrs_plan_desc {
   const int32_t *d_row_map; /* packed row -> output row, NULL for the identity order */
   int32_t packing;        /* SRBCRS_PACK_* */
   int32_t dup_policy;     /* SRBCRS_DUP_* */
+  int64_t stored_values;  /* values in the compact copy of val (-1: no copy) */
 } srbcrs_plan_desc;
 int srbcrs_plan_get(const srbcrs_plan *plan, srbcrs_plan_desc *out);
 
@@ -224,7 +225,18 @@ typedef struct srbcrs_run_opts {
   int32_t wg_cols;
   int32_t grid_order;
   int32_t windows_per_wave;
+  int32_t a_operand;
 } srbcrs_run_opts;
+
+/* a_operand: where the kernel reads the block values from.  Both give the
+ * same bits.  COMPACT reads the plan's compact copy (per 32 block positions
+ * a {mask, base} word plus the stored values; built at plan creation); DENSE
+ * reads the reference-layout value array.  DEFAULT = COMPACT when the plan
+ * has the copy (it is skipped when it would not fit) and at most half of the
+ * block positions hold values, else DENSE. */
+#define SRBCRS_A_DEFAULT 0
+#define SRBCRS_A_COMPACT 1
+#define SRBCRS_A_DENSE 2
 
 #define SRBCRS_GRID_DEFAULT 0
 #define SRBCRS_GRID_CHUNK_MAJOR 1

@@ -111,10 +111,11 @@ class Plan:
         return self.nnz / max(1, self.total_blocks * self.blk_h * self.blk_w)
 
     def run(self, dense: Tensor, out: Optional[Tensor] = None, depth: int = 0, tile_b: int = 0, wg_cols: int = 0,
-            grid_order: int = 0, windows_per_wave: int = 0) -> Tensor:
+            grid_order: int = 0, windows_per_wave: int = 0, a_operand: str = "default") -> Tensor:
         """out[:num_nodes] = A @ dense on the current stream.  The keyword
         knobs are the kernel template parameters (srbcrs_run_opts; 0 =
-        default; grid_order 1 = chunk-major, 2 = window-major)."""
+        default; grid_order 1 = chunk-major, 2 = window-major; a_operand
+        "compact" / "dense" picks the block-value copy the kernel reads)."""
         if out is None:
             out = torch.empty((self.num_nodes, dense.shape[1]), dtype=torch.float32, device=dense.device)
         if dense.dtype != torch.float32 or out.dtype != torch.float32:
@@ -123,7 +124,8 @@ class Plan:
             raise RuntimeError("dense and out must be row-major 2-D")
         if out.shape[1] != dense.shape[1]:
             raise RuntimeError("out and dense must have the same number of columns")
-        opts = _capi.RunOpts(int(depth), int(tile_b), int(wg_cols), int(grid_order), int(windows_per_wave))
+        opts = _capi.RunOpts(int(depth), int(tile_b), int(wg_cols), int(grid_order), int(windows_per_wave),
+                             _capi.A_OPERANDS[a_operand])
         with torch.cuda.device(self.device):
             _capi.check(_capi.lib().srbcrs_run_ex(self._h, dense.data_ptr(), int(dense.shape[0]), int(dense.shape[1]),
                                                   int(dense.stride(0)), out.data_ptr(), int(out.stride(0)),

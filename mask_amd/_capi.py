@@ -55,6 +55,7 @@ class PlanDesc(ctypes.Structure):
         ("d_row_map", ctypes.c_void_p),
         ("packing", ctypes.c_int32),
         ("dup_policy", ctypes.c_int32),
+        ("stored_values", ctypes.c_int64),
     ]
 
 
@@ -71,7 +72,11 @@ DUPS = {"last": 0, "sum": 1}
 
 class RunOpts(ctypes.Structure):
     _fields_ = [("depth", ctypes.c_int32), ("tile_b", ctypes.c_int32), ("wg_cols", ctypes.c_int32),
-                ("grid_order", ctypes.c_int32), ("windows_per_wave", ctypes.c_int32)]
+                ("grid_order", ctypes.c_int32), ("windows_per_wave", ctypes.c_int32),
+                ("a_operand", ctypes.c_int32)]
+
+
+A_OPERANDS = {"default": 0, "compact": 1, "dense": 2}
 
 
 class SrbcrsError(RuntimeError):

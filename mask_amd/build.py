@@ -60,9 +60,11 @@ def build(verbose: bool = False) -> Path:
             print(out)
         return str(obj)
 
-    with ThreadPoolExecutor(max_workers=4) as ex:
+    with ThreadPoolExecutor(max_workers=6) as ex:
         gen = [ex.submit(build_generated_one, bm, bk) for bm, bk in GENERATED_SHAPES]
-        objs = list(ex.map(compile_obj, ("srbcrs_kernels.hip", "srbcrs_capi.cpp", "srbcrs_pack.cpp", "srbcrs_convert.hip")))
+        objs = list(ex.map(compile_obj, ("srbcrs_stream_compact.hip", "srbcrs_stream_dense.hip", "srbcrs_kernels.hip",
+                                         "srbcrs_capi.cpp", "srbcrs_pack.cpp", "srbcrs_convert.hip",
+                                         "srbcrs_compact.hip")))
         for f in gen:
             f.result()
     tmp = LIB.with_suffix(".so.tmp")

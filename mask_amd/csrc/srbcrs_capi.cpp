@@ -415,6 +415,10 @@ struct srbcrs_plan {
   int32_t n_zero_rows = 0;
   // edge maps of a plan converted on the device (host vectors above are empty then)
   int32_t *d_e2r = nullptr, *d_e2c = nullptr, *d_bp = nullptr;
+  // compact copy of val that the SpMM reads by default (null: read val)
+  uint2* d_awords = nullptr;
+  float* d_apacked = nullptr;
+  int64_t n_apacked = 0;
 
   void free_schedule() {
     dev_free(d_group_off);
@@ -439,6 +443,8 @@ struct srbcrs_plan {
     dev_free(d_e2r);
     dev_free(d_e2c);
     dev_free(d_bp);
+    dev_free(d_awords);
+    dev_free(d_apacked);
     if (switched) (void)hipSetDevice(cur);
   }
 };
@@ -590,6 +596,23 @@ void create_on_device(srbcrs_plan& plan, const int32_t* rowptr, const int32_t* c
   plan.sched.policy = "row";
 }
 
+// Compact copy of the block values (srbcrs_compact.hip).  A plan too large
+// for it, or a device without the memory, keeps reading val.
+void build_compact(srbcrs_plan& plan, hipStream_t st) {
+  if (plan.total == 0) return;
+  srbcrs::CompactOut c;
+  const hipError_t e = srbcrs::device_compact(plan.d_val, plan.total, plan.blk_h, plan.blk_w, conv_alloc,
+                                              conv_free, nullptr, st, c);
+  if (e == hipErrorOutOfMemory || e == hipErrorInvalidValue) {
+    (void)hipGetLastError();
+    return;
+  }
+  hip_check(e, "compact block values");
+  plan.d_awords = c.words;
+  plan.d_apacked = c.packed;
+  plan.n_apacked = c.n_packed;
+}
+
 }  // namespace
 
 extern "C" {
@@ -679,6 +702,7 @@ int srbcrs_plan_create_ex(const int32_t* rowptr, const int32_t* colind, const fl
       plan->canonical = true;
       plan->packed_rows = num_nodes;
       create_on_device(*plan, rowptr, colind, values, st);
+      build_compact(*plan, st);
       *out = plan.release();
       return;
     }
@@ -711,6 +735,7 @@ int srbcrs_plan_create_ex(const int32_t* rowptr, const int32_t* colind, const fl
     plan->canonical = canonical;
     if (!canonical) {
       create_packed(*plan, rp, ci, vv, o);
+      build_compact(*plan, st);
       *out = plan.release();
       return;
     }
@@ -733,6 +758,7 @@ int srbcrs_plan_create_ex(const int32_t* rowptr, const int32_t* colind, const fl
     plan->d_sidx = upload(sidx);
     plan->d_val = upload(val);
     plan->sched.policy = "row";
+    build_compact(*plan, st);
     *out = plan.release();
   });
 }
@@ -757,6 +783,7 @@ int srbcrs_plan_get(const srbcrs_plan* plan, srbcrs_plan_desc* out) {
     out->d_row_map = plan->d_rowmap;
     out->packing = plan->packing;
     out->dup_policy = plan->dup_policy;
+    out->stored_values = plan->d_awords || plan->total == 0 ? plan->n_apacked : -1;
   });
 }
 
@@ -974,8 +1001,20 @@ int srbcrs_run_ex(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int
         fail(SRBCRS_EINVAL, "windows_per_wave must be in [0, 4096] (got %d)", opts->windows_per_wave);
       ro.windows_per_wave = opts->windows_per_wave ? opts->windows_per_wave : 1;
       if (opts->tile_b) max_vec = opts->tile_b / 16;
+      if (opts->a_operand < 0 || opts->a_operand > 2)
+        fail(SRBCRS_EINVAL, "a_operand must be 0, 1 or 2 (got %d)", opts->a_operand);
     }
     if (!plan) fail(SRBCRS_EINVAL, "plan is NULL");
+    if (opts && opts->a_operand == SRBCRS_A_COMPACT && !plan->d_awords && plan->total > 0)
+      fail(SRBCRS_ESTATE, "the plan has no compact copy of its block values");
+    {
+      // default: the compact copy when at most half of the block positions
+      // hold values (it skips the zeros; at full blocks it only adds the
+      // mask words and the decode: banded, fill 1.0, runs 13 % slower on it)
+      const int a_op = opts ? opts->a_operand : SRBCRS_A_DEFAULT;
+      const bool sparse_blocks = 2 * plan->n_apacked <= plan->total * (int64_t)plan->blk_h * plan->blk_w;
+      ro.a_compact = a_op == SRBCRS_A_COMPACT || (a_op == SRBCRS_A_DEFAULT && sparse_blocks);
+    }
     int cur = 0;
     hip_check(hipGetDevice(&cur), "hipGetDevice");
     if (cur != plan->device) fail(SRBCRS_ESTATE, "plan lives on device %d, current device is %d", plan->device, cur);
@@ -998,7 +1037,7 @@ int srbcrs_run_ex(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int
                        (reinterpret_cast<uintptr_t>(d_C) % (4 * vec))))
       vec /= 2;
     srbcrs::StreamArgs a{d_B, d_C, nullptr, plan->d_sidx, plan->d_val, (int)plan->packed_rows, (int)N, ldb, ldc,
-                         plan->blk_h, plan->d_rowmap};
+                         plan->blk_h, plan->d_rowmap, plan->d_awords, plan->d_apacked};
     if (plan->n_zero_rows)
       hip_check(srbcrs::launch_zero_rows(d_C, plan->d_zero_rows, plan->n_zero_rows, (int)N, ldc, st),
                 "launch zero_rows");

@@ -34,4 +34,15 @@ typedef void (*DeviceFree)(void* ctx, void* p);
 hipError_t device_convert(const DeviceConvertIn& in, DeviceConvertOut& out, DeviceAlloc alloc,
                           DeviceFree dfree, void* ctx, hipStream_t st);
 
+// Compact copy of the block values (srbcrs_compact.hip): per 32 logical
+// positions of a block one {mask, base} word, and the stored values.
+struct CompactOut {
+  uint2* words = nullptr;   // n_blocks * BH*BW/32
+  float* packed = nullptr;  // n_packed (at least one element allocated)
+  int64_t n_packed = 0;
+};
+
+hipError_t device_compact(const float* val, int64_t n_blocks, int blk_h, int blk_w, DeviceAlloc alloc,
+                          DeviceFree dfree, void* ctx, hipStream_t st, CompactOut& out);
+
 }  // namespace srbcrs

@@ -13,6 +13,7 @@ struct RunOpts {
   int wg_cols = 128;         // columns per workgroup (0 = up to 4 waves)
   int chunk_major = 1;       // grid order: 0 window-major, 1 chunk-major
   int windows_per_wave = 1;  // row schedule: consecutive windows streamed per wave
+  int a_compact = 1;         // read A from the compact copy when the plan has one
 };
 
 // Operands shared by every SR-BCRS launch.
@@ -26,6 +27,8 @@ struct StreamArgs {
   int64_t ldb, ldc;
   int blk_h;        // 16 (16x8 blocks) or 32 (32x32 blocks)
   const int* rowmap = nullptr;  // packed row -> output row (null = identity); M counts packed rows
+  const uint2* a_words = nullptr;   // compact A (null = read val)
+  const float* a_packed = nullptr;
 };
 
 struct TaskTable {
@@ -63,6 +66,15 @@ hipError_t launch_row(const StreamArgs& a, const int* soff, int Mo, int vec, con
                       hipStream_t st);
 hipError_t launch_tasks(const StreamArgs& a, const TaskTable& t, int vec, const RunOpts& o,
                         hipStream_t st);
+// per A source (srbcrs_stream_dense.hip / srbcrs_stream_compact.hip)
+hipError_t launch_row_dense(const StreamArgs& a, const int* soff, int Mo, int vec, const RunOpts& o,
+                            hipStream_t st);
+hipError_t launch_tasks_dense(const StreamArgs& a, const TaskTable& t, int vec, const RunOpts& o,
+                              hipStream_t st);
+hipError_t launch_row_compact(const StreamArgs& a, const int* soff, int Mo, int vec, const RunOpts& o,
+                              hipStream_t st);
+hipError_t launch_tasks_compact(const StreamArgs& a, const TaskTable& t, int vec, const RunOpts& o,
+                                hipStream_t st);
 hipError_t launch_reduce(const ReduceArgs& a, int vec, hipStream_t st);
 hipError_t launch_csr(const CsrArgs& a, int vec, hipStream_t st);
 hipError_t launch_zero_rows(float* C, const int* rows, int n_rows, int N, int64_t ldc, hipStream_t st);

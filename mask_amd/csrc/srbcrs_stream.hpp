@@ -88,24 +88,91 @@ struct Frag {
   V b1[G];       // B[sidx[8u+2k+1]][cols of g]
 };
 
-template <int BH, int BW, int VEC, int G>
-__device__ __forceinline__ void load_frag(Frag<BH / 16, VEC, G>& f, const float* __restrict__ B,
-                                          const float* __restrict__ val, int64_t unit, int2 rows,
-                                          const int (&a_off)[BW / 8][BH / 16], int64_t ldb,
-                                          int col0) {
-  typedef Shape<BH, BW> S;
-  typedef typename VecT<VEC>::type V;
-  const int64_t blk = unit / S::Q;
-  const int q = (int)(unit % S::Q);
-  const float* vb = val + blk * S::SIZE;
+// A-operand sources.  Both hand the MFMA the same fragments, bit for bit.
+//
+// DenseA reads the block values in the reference's layout (val, BH*BW
+// swizzled fp32 per block): the lane's two values are adjacent, one 8-byte
+// load per row half.
+//
+// CompactA reads them from a compact copy: for every 32 logical positions
+// o = BW*r + c of a block one word {mask, base}, bit t of mask marking a
+// stored value at position 32*w + t, whose index in `packed` is base plus
+// the number of mask bits below t; unmarked positions are +0.0f.  At the
+// low block fills of graph matrices most of the dense array is zeros, so
+// this cuts the A bytes a column chunk re-reads by up to ~10x.  The word is
+// fetched one ring slot ahead (Meta), so the value loads it steers issue
+// with the unit's B loads.
+struct DenseA {
+  const float* __restrict__ val;
+  template <int H> struct Meta {};
+  template <int BH, int BW>
+  __device__ __forceinline__ Meta<BH / 16> meta(int64_t, int) const { return {}; }
+  template <int BH, int BW>
+  __device__ __forceinline__ void load(f2 (&a)[BH / 16], int64_t unit, const Meta<BH / 16>&,
+                                       const int (&a_off)[BW / 8][BH / 16], int) const {
+    typedef Shape<BH, BW> S;
+    const int64_t blk = unit / S::Q;
+    const int q = (int)(unit % S::Q);
+    const float* vb = val + blk * S::SIZE;
 #pragma unroll
-  for (int h = 0; h < S::H; ++h) {
-    int off = a_off[0][h];
+    for (int h = 0; h < S::H; ++h) {
+      int off = a_off[0][h];
 #pragma unroll
-    for (int qq = 1; qq < S::Q; ++qq)
-      if (q == qq) off = a_off[qq][h];
-    f.a[h] = *reinterpret_cast<const f2*>(vb + off);
+      for (int qq = 1; qq < S::Q; ++qq)
+        if (q == qq) off = a_off[qq][h];
+      a[h] = *reinterpret_cast<const f2*>(vb + off);
+    }
   }
+};
+
+struct CompactA {
+  const uint2* __restrict__ words;
+  const float* __restrict__ packed;
+  template <int H> struct Meta { uint2 w[H]; };
+  // logical position of the lane's first value in unit q, row half h
+  template <int BW>
+  __device__ __forceinline__ static int pos(int h, int q, int lane) {
+    return BW * (16 * h + (lane & 15)) + 8 * q + 2 * (lane >> 4);
+  }
+  template <int BH, int BW>
+  __device__ __forceinline__ Meta<BH / 16> meta(int64_t unit, int lane) const {
+    typedef Shape<BH, BW> S;
+    const int64_t blk = unit / S::Q;
+    const int q = (int)(unit % S::Q);
+    Meta<S::H> m;
+#pragma unroll
+    for (int h = 0; h < S::H; ++h) m.w[h] = words[blk * (S::SIZE / 32) + (pos<BW>(h, q, lane) >> 5)];
+    return m;
+  }
+  template <int BH, int BW>
+  __device__ __forceinline__ void load(f2 (&a)[BH / 16], int64_t unit, const Meta<BH / 16>& m,
+                                       const int (&)[BW / 8][BH / 16], int lane) const {
+    typedef Shape<BH, BW> S;
+    const int q = (int)(unit % S::Q);
+#pragma unroll
+    for (int h = 0; h < S::H; ++h) {
+      const int bit = pos<BW>(h, q, lane) & 31;   // even, so bit + 1 is in the same word
+      const uint32_t mask = m.w[h].x;
+      const uint32_t n = m.w[h].y + (uint32_t)__builtin_popcount(mask & ((1u << bit) - 1u));
+      const uint32_t b0 = (mask >> bit) & 1u, b1 = (mask >> (bit + 1)) & 1u;
+      float v0 = 0.f, v1 = 0.f;
+      if (b0) v0 = packed[n];
+      if (b1) v1 = packed[n + b0];
+      a[h] = f2{v0, v1};
+    }
+  }
+};
+
+// Issue the loads of one unit: the A fragment (through the A source) and the
+// lane's B vectors of rows rows.x (k-step 0) and rows.y (k-step 1).
+template <int BH, int BW, int VEC, int G, class AF>
+__device__ __forceinline__ void load_frag(Frag<BH / 16, VEC, G>& f, const float* __restrict__ B,
+                                          const AF& asrc, int64_t unit, int2 rows,
+                                          const typename AF::template Meta<BH / 16>& am,
+                                          const int (&a_off)[BW / 8][BH / 16], int64_t ldb,
+                                          int col0, int lane) {
+  typedef typename VecT<VEC>::type V;
+  asrc.template load<BH, BW>(f.a, unit, am, a_off, lane);
   const float* r0 = B + (int64_t)rows.x * ldb + col0;
   const float* r1 = B + (int64_t)rows.y * ldb + col0;
 #pragma unroll
@@ -231,10 +298,10 @@ __device__ __forceinline__ void flush_task(const Src& src, int t, f4 (&acc)[BH /
 // instantiation (amdgpu_waves_per_eu, 98 registers instead of 146) made it
 // slower on the GPU (GCN N=256 1.83 -> 2.02 ms), because the tighter budget
 // delays the ring's loads.
-template <class Src, int BH, int BW, int VEC, int G, int WAVES, int DEPTH>
+template <class Src, int BH, int BW, int VEC, int G, int WAVES, int DEPTH, class AF>
 __global__ __launch_bounds__(64 * WAVES) void spmm_stream(
     Src src, const float* __restrict__ B, float* __restrict__ C, float* __restrict__ partial,
-    const int* __restrict__ sidx, const float* __restrict__ val, int M, int N, int64_t ldb,
+    const int* __restrict__ sidx, AF asrc, int M, int N, int64_t ldb,
     int64_t ldc, int n_chunks, int chunk_major) {
   typedef Shape<BH, BW> S;
   constexpr int WCOLS = 16 * VEC * G;
@@ -271,14 +338,17 @@ __global__ __launch_bounds__(64 * WAVES) void spmm_stream(
       for (int h = 0; h < S::H; ++h) a_off[q][h] = swizzle_2_2_3(BW * (16 * h + i) + 8 * q + 2 * k);
     Frag<S::H, VEC, G> f[DEPTH];
     int2 idx[DEPTH];
+    typename AF::template Meta<S::H> am[DEPTH];
     const int64_t last = ue - 1;
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
       const int64_t u = us + d < last ? us + d : last;
       const int2 rows = *reinterpret_cast<const int2*>(sidx + u * 8 + 2 * k);
-      load_frag<BH, BW, VEC, G>(f[d], B, val, u, rows, a_off, ldb, col0);
+      load_frag<BH, BW, VEC, G>(f[d], B, asrc, u, rows, asrc.template meta<BH, BW>(u, lane), a_off, ldb,
+                                col0, lane);
       const int64_t nu = us + DEPTH + d < last ? us + DEPTH + d : last;
       idx[d] = *reinterpret_cast<const int2*>(sidx + nu * 8 + 2 * k);
+      am[d] = asrc.template meta<BH, BW>(nu, lane);
     }
     for (int64_t base = us; base < ue; base += DEPTH) {
 #pragma unroll
@@ -294,9 +364,10 @@ __global__ __launch_bounds__(64 * WAVES) void spmm_stream(
         }
         const int64_t nu = u + DEPTH;
         if (nu < ue) {
-          load_frag<BH, BW, VEC, G>(f[d], B, val, nu, idx[d], a_off, ldb, col0);
+          load_frag<BH, BW, VEC, G>(f[d], B, asrc, nu, idx[d], am[d], a_off, ldb, col0, lane);
           const int64_t nn = nu + DEPTH < last ? nu + DEPTH : last;
           idx[d] = *reinterpret_cast<const int2*>(sidx + nn * 8 + 2 * k);
+          am[d] = asrc.template meta<BH, BW>(nn, lane);
         }
       }
     }
@@ -339,14 +410,17 @@ __global__ __launch_bounds__(256) void segment_reduce(const float* __restrict__ 
   }
 }
 
-// Zero the listed output rows (rows a sparse-row packing leaves out).
-__global__ __launch_bounds__(256) void zero_rows(float* __restrict__ C, const int* __restrict__ rows,
+// Zero the listed output rows (rows a sparse-row packing leaves out).  A
+// template (T = float) so that every translation unit including this header
+// may instantiate it.
+template <class T>
+__global__ __launch_bounds__(256) void zero_rows(T* __restrict__ C, const int* __restrict__ rows,
                                                  int n_rows, int N, int64_t ldc) {
   const int64_t total = (int64_t)n_rows * N;
   for (int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; id < total;
        id += (int64_t)gridDim.x * blockDim.x) {
     const int64_t i = id / N, c = id % N;
-    C[(int64_t)rows[i] * ldc + c] = 0.f;
+    C[(int64_t)rows[i] * ldc + c] = T(0);
   }
 }
 

@@ -161,8 +161,9 @@ int launch(const Src& src, int n_groups, const float* B, float* C, float* partia
   const long long nwg = (long long)n_groups * n_chunks;
   if (nwg == 0) return 0;
   if (nwg > 0x7fffffffLL) return -1;
-  hipLaunchKernelGGL((srbcrs::spmm_stream<Src, kBH, kBW, kVEC, kG, kWAVES, kDEPTH>), dim3((unsigned)nwg),
-                     dim3(64 * kWAVES), 0, st, src, B, C, partial, sidx, val, M, N, (int64_t)ldb,
+  hipLaunchKernelGGL((srbcrs::spmm_stream<Src, kBH, kBW, kVEC, kG, kWAVES, kDEPTH, srbcrs::DenseA>),
+                     dim3((unsigned)nwg), dim3(64 * kWAVES), 0, st, src, B, C, partial, sidx,
+                     srbcrs::DenseA{{val}}, M, N, (int64_t)ldb,
                      (int64_t)ldc, n_chunks, kChunkMajor);
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }}
@@ -216,7 +217,7 @@ extern "C" int sparsene_generated_zero_rows(float* C, const int* rows, int n_row
   long long total = (long long)n_rows * N;
   long long blocks = (total + 255) / 256;
   if (blocks > 65536) blocks = 65536;
-  hipLaunchKernelGGL(srbcrs::zero_rows, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+  hipLaunchKernelGGL(srbcrs::zero_rows<float>, dim3((unsigned)blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
                      C, rows, n_rows, N, (int64_t)ldc);
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }}

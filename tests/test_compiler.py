@@ -114,7 +114,7 @@ def test_emitted_source_structure_and_determinism():
     for needle in ("#define SPARSENE_GENERATED_TILE_B 64", "#define SPARSENE_GENERATED_SUPPORTS_TASK_MAPPING 1",
                    "#define SPARSENE_GENERATED_WAVE_SIZE 64", "#define SPARSENE_GENERATED_PIPELINE_DEPTH 4",
                    "constexpr int NNZ_HINT = 7;", '#include "srbcrs_stream.hpp"',
-                   "srbcrs::spmm_stream<Src, kBH, kBW, kVEC, kG, kWAVES, kDEPTH>",
+                   "srbcrs::spmm_stream<Src, kBH, kBW, kVEC, kG, kWAVES, kDEPTH, srbcrs::DenseA>",
                    'extern "C" int sparsene_generated_run(', 'extern "C" int sparsene_generated_run_tasks(',
                    'extern "C" int sparsene_generated_reduce('):
         assert needle in src, needle
