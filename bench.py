@@ -50,6 +50,8 @@ def parse():
     ap.add_argument("--wg-cols", type=int, default=0, help="kernel knob: columns per workgroup")
     ap.add_argument("--grid-order", type=int, default=0, help="kernel knob: 1 chunk-major, 2 window-major")
     ap.add_argument("--wpw", type=int, default=0, help="kernel knob: row windows streamed per wave")
+    ap.add_argument("--no-tune", action="store_true",
+                    help="skip srbcrs_plan_tune (the one-time launch-setting search run before the warm-up)")
     ap.add_argument("--a-operand", default="default", choices=["default", "compact", "dense"],
                     help="block-value copy the kernel reads (default: compact when blocks are at most half full)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
@@ -89,6 +91,10 @@ def gcn_forward_bench(args):
     plan.set_schedule("split", 0)
     h1 = torch.empty((m.M, 256), device=dev)
     out = torch.empty((m.M, 64), device=dev)
+    tuned = {}
+    if not args.no_tune:   # one-time launch-setting search per width, before the warm-up
+        tuned["N256"] = plan.tune(X @ w1, h1)
+        tuned["N64"] = plan.tune(torch.relu(h1) @ w2, out)
 
     def fwd():
         plan.run(X @ w1, h1)
@@ -122,10 +128,15 @@ def gcn_forward_bench(args):
         "metric": "GCN two-layer forward time (gcn-232965, features 512, hidden 256, out 64)",
         "value": round(ms, 4), "unit": "ms", "higher_is_better": False, "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "dtype": "f32", "data": "synthetic R-MAT graph + N(0,1) features (seeded)",
-        "config": {"workload": m.name, "nodes": m.M, "nnz": m.nnz, "schedule": "split:auto"},
+        "config": {"workload": m.name, "nodes": m.M, "nnz": m.nnz, "schedule": "split:auto", "tuned": tuned},
         "spmm_ms": {"N256": round(sp256, 4), "N64": round(sp64, 4)},
         "spmm_gflops": {"N256": round(2 * m.nnz * 256 / sp256 / 1e6, 1), "N64": round(2 * m.nnz * 64 / sp64 / 1e6, 1)},
     }), flush=True)
+
+
+def tuned_knobs(t, tune_s):
+    return {"depth": t["depth"], "tile_b": 0, "wg_cols": t["wg_cols"], "grid_order": t["grid_order"],
+            "windows_per_wave": 1, "a_operand": t["a_operand"], "tuned": True, "tune_s": round(tune_s, 3)}
 
 
 def a_operand_used(plan, requested):
@@ -190,6 +201,14 @@ def main():
     plan.set_schedule(name, int(param) if param else 0)
     max_col = plan.max_col
 
+    explicit = bool(args.depth or args.tile_b or args.wg_cols or args.grid_order or args.wpw
+                    or args.a_operand != "default")
+    tuned, tune_s = None, 0.0
+    if args.kernel == "srbcrs" and not args.no_tune and not explicit:
+        t0 = time.time()
+        tuned = plan.tune(B, C)   # outside the timed region, like the conversion
+        torch.cuda.synchronize()
+        tune_s = time.time() - t0
     if args.kernel == "srbcrs":
         step = lambda: plan.run(B, C, depth=args.depth, tile_b=args.tile_b, wg_cols=args.wg_cols,
                                 grid_order=args.grid_order, windows_per_wave=args.wpw, a_operand=args.a_operand)
@@ -216,6 +235,10 @@ def main():
     flops = 2.0 * m.nnz * N
     gflops = flops / t_s / 1e9
 
+    knobs = tuned_knobs(tuned, tune_s) if tuned else \
+        {"depth": args.depth or 2, "tile_b": args.tile_b, "wg_cols": args.wg_cols or 128,
+         "grid_order": args.grid_order or 1, "windows_per_wave": args.wpw or 1,
+         "a_operand": a_operand_used(plan, args.a_operand), "tuned": False}
     ab = algorithmic_bytes(m.M, N, Mo, nb, m.nnz, args.kernel)
     compulsory = (nb * (8 * 4 + 128 * 4) + 4 * (Mo + 1) if args.kernel == "srbcrs" else 8 * m.nnz) \
         + m.K * N * 4 + m.M * N * 4
@@ -240,16 +263,12 @@ def main():
                    "block_fill": round(m.nnz / (128 * max(nb, 1)), 4), "kernel": args.kernel,
                    "schedule": f"{plan.policy[0]}:{plan.policy[1]}", "seed": m.seed, "row_order": args.row_order,
                    "conversion_s": round(conv_s, 3), "meta": m.meta,
-                   "knobs": {"depth": args.depth or 2, "tile_b": args.tile_b, "wg_cols": args.wg_cols or 128,
-                             "grid_order": args.grid_order or 1, "windows_per_wave": args.wpw or 1,
-                             "a_operand": a_operand_used(plan, args.a_operand)}},
+                   "knobs": knobs},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(m.name, N, args.kernel,
-                                                 not (args.depth or args.tile_b or args.wg_cols or args.grid_order
-                                                      or args.wpw) and args.schedule == "auto"
-                                                 and args.a_operand == "default"
-                                                 and args.row_order == "identity" and not args.mtx),
+                     "traffic": measured_traffic(m.name, N, args.kernel, knobs
+                                                 if args.schedule == "auto" and not args.tile_b and not args.wpw
+                                                 and args.row_order == "identity" and not args.mtx else None),
                      "algorithmic_bytes": int(ab), "compulsory_bytes": int(compulsory),
                      "compulsory_frac": round(compulsory / t_s / 1e9 / HBM_PEAK_GBS, 4),
                      "mfma_padded_tflops": round(padded_flops / t_s / 1e12, 3),
@@ -266,20 +285,25 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-def measured_traffic(workload, N, kernel, default_knobs):
+def measured_traffic(workload, N, kernel, knobs):
     """HBM bytes per launch of the dominant kernel from the committed
     rocprofv3 PMC summary (FETCH_SIZE and WRITE_SIZE runs, scaled by the
-    copy-kernel calibration), when one exists for this workload and the
-    default kernel configuration; None otherwise."""
-    if kernel != "srbcrs" or not default_knobs:
+    copy-kernel calibration), when one exists for this workload and was
+    profiled with the launch settings this run used (its "knobs:" line);
+    None otherwise."""
+    if kernel != "srbcrs" or knobs is None:
         return None
     path = ROOT / "profiles" / f"spmm_stream_{workload.replace('^', '')}_N{N}.md"
     if not path.exists():
         return None
+    traffic, prof_knobs = None, None
     for line in path.read_text().splitlines():
         if line.startswith("traffic_bytes:"):
-            return int(line.split(":", 1)[1])
-    return None
+            traffic = int(line.split(":", 1)[1])
+        elif line.startswith("knobs:"):
+            prof_knobs = dict(kv.split("=") for kv in line.split(":", 1)[1].split())
+    want = {k: str(knobs[k]) for k in ("depth", "wg_cols", "grid_order", "a_operand")}
+    return traffic if prof_knobs == want else None
 
 
 def datasets_soff(plan):

@@ -247,6 +247,19 @@ int srbcrs_run_ex(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int
                   float *d_C, int64_t ldc, int64_t c_rows, const srbcrs_run_opts *opts,
                   void *stream);
 
+/* Time the candidate launch settings (wg_cols 128 / 64 x depth 2 / 4 / 8,
+ * chunk-major, x the compact and dense A operands) on this plan for a dense
+ * width N, reps timed launches each after one warm-up, on `stream`, and
+ * keep the fastest: later srbcrs_run calls, and srbcrs_run_ex calls whose
+ * knobs are all 0, at that N use it until the schedule changes.  C is
+ * overwritten (with the product).  Every candidate gives the same bits, so
+ * tuning changes only the time.  best (may be NULL) receives the choice.
+ * No reference counterpart: the reference fixes its launch shape at build
+ * time (strategy_agent.py:81-130 picks it offline). */
+int srbcrs_plan_tune(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int64_t ldb,
+                     float *d_C, int64_t ldc, int64_t c_rows, int32_t reps, srbcrs_run_opts *best,
+                     void *stream);
+
 /* ---- CSR fallback for low block density: C[r, :] = sum_e val[e] *
  * B[col[e], :], fp32, edge order.  The arithmetic of csr_spmm_value_kernel
  * (SRK:66-105), one wave64 per row.  max_col (host-known bound on colind,

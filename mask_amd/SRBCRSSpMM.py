@@ -94,6 +94,7 @@ class Plan:
         self.total_blocks = int(d.total_blocks)
         self.max_col = int(d.max_col)
         self.policy = ("row", 0)
+        self.tuned_widths = set()   # widths srbcrs_plan_tune chose settings for (current schedule)
 
     @property
     def handle(self):
@@ -105,6 +106,7 @@ class Plan:
         with torch.cuda.device(self.device):
             _capi.check(_capi.lib().srbcrs_plan_set_schedule(self._h, policy.encode(), int(param)))
         self.policy = (policy, param)
+        self.tuned_widths = set()
 
     def block_fill(self) -> float:
         """nnz / (blocks * blk_h * blk_w): the stored-value density."""
@@ -131,6 +133,27 @@ class Plan:
                                                   int(dense.stride(0)), out.data_ptr(), int(out.stride(0)),
                                                   int(out.shape[0]), ctypes.byref(opts), _stream_handle(self.device)))
         return out
+
+    def tune(self, dense: Tensor, out: Optional[Tensor] = None, reps: int = 3) -> dict:
+        """Time the launch candidates for dense.shape[1] on this plan (see
+        srbcrs_plan_tune) and keep the fastest for later default-knob runs
+        at that width; returns the choice.  out (or a scratch tensor) is
+        overwritten with A @ dense."""
+        if out is None:
+            out = torch.empty((self.num_nodes, dense.shape[1]), dtype=torch.float32, device=dense.device)
+        if dense.dtype != torch.float32 or out.dtype != torch.float32 or dense.dim() != 2 or out.dim() != 2 \
+                or dense.stride(1) != 1 or out.stride(1) != 1 or out.shape[1] != dense.shape[1]:
+            raise RuntimeError("dense and out must be row-major 2-D float32 with the same number of columns")
+        best = _capi.RunOpts()
+        with torch.cuda.device(self.device):
+            _capi.check(_capi.lib().srbcrs_plan_tune(self._h, dense.data_ptr(), int(dense.shape[0]),
+                                                     int(dense.shape[1]), int(dense.stride(0)), out.data_ptr(),
+                                                     int(out.stride(0)), int(out.shape[0]), int(reps),
+                                                     ctypes.byref(best), _stream_handle(self.device)))
+        self.tuned_widths.add(int(dense.shape[1]))
+        inv = {v: k for k, v in _capi.A_OPERANDS.items()}
+        return {"depth": best.depth, "wg_cols": best.wg_cols, "grid_order": best.grid_order,
+                "a_operand": inv[best.a_operand]}
 
     def row_order(self):
         """The plan's row order (new -> original) as a numpy array."""
@@ -287,7 +310,10 @@ def _run(dense: Tensor, row_window_offset: Tensor, tcblocktile_id: Tensor, tcblo
     sched = _schedule_from_exeplan(exeplan)
     entry.plan.set_schedule(*(sched or ("row", 0)))
     out = torch.empty((entry.num_nodes, n), dtype=torch.float32, device=dense.device)
-    entry.plan.run(dense, out)
+    if os.environ.get("SPARSENE_SRBCRS_AUTOTUNE", "0") == "1" and n not in entry.plan.tuned_widths:
+        entry.plan.tune(dense, out)   # once per (width, schedule); the product lands in out
+    else:
+        entry.plan.run(dense, out)
     return [out]
 
 

@@ -28,6 +28,7 @@ EXPORTS = (
     "srbcrs_schedule_build", "srbcrs_schedule_info", "srbcrs_schedule_export", "srbcrs_schedule_destroy",
     "srbcrs_plan_set_schedule", "srbcrs_run", "srbcrs_run_ex", "srbcrs_csr_spmm",
     "srbcrs_row_order", "srbcrs_pack_count", "srbcrs_pack_fill", "srbcrs_plan_create_ex", "srbcrs_plan_row_order",
+    "srbcrs_plan_tune",
 )
 
 _i32p = ctypes.POINTER(ctypes.c_int32)
@@ -126,6 +127,8 @@ def lib() -> ctypes.CDLL:
         "srbcrs_plan_create_ex": ([_vp, _vp, _vp, _i32, _i64, ctypes.POINTER(PackOpts), _i32, _vp,
                                    ctypes.POINTER(_vp)], ctypes.c_int),
         "srbcrs_plan_row_order": ([_vp, _vp, _i32, _i32p], ctypes.c_int),
+        "srbcrs_plan_tune": ([_vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i32, ctypes.POINTER(RunOpts), _vp],
+                             ctypes.c_int),
         "srbcrs_csr_spmm": ([_vp, _vp, _vp, _i32, _i64, _i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp],
                             ctypes.c_int),
     }

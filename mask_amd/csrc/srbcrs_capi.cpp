@@ -12,6 +12,7 @@
 #include <new>
 #include <string>
 #include <thread>
+#include <map>
 #include <vector>
 
 #include "../../include/srbcrs.h"
@@ -419,6 +420,9 @@ struct srbcrs_plan {
   uint2* d_awords = nullptr;
   float* d_apacked = nullptr;
   int64_t n_apacked = 0;
+  // launch settings chosen by srbcrs_plan_tune, per dense width N, for the
+  // current schedule (cleared when it changes)
+  std::map<int64_t, srbcrs_run_opts> tuned;
 
   void free_schedule() {
     dev_free(d_group_off);
@@ -594,6 +598,10 @@ void create_on_device(srbcrs_plan& plan, const int32_t* rowptr, const int32_t* c
             "copy soff");
   hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
   plan.sched.policy = "row";
+}
+
+bool all_default(const srbcrs_run_opts& o) {
+  return !o.depth && !o.tile_b && !o.wg_cols && !o.grid_order && !o.windows_per_wave && !o.a_operand;
 }
 
 // Compact copy of the block values (srbcrs_compact.hip).  A plan too large
@@ -961,6 +969,7 @@ int srbcrs_plan_set_schedule(srbcrs_plan* plan, const char* policy, int32_t para
     Schedule* s = build_schedule(plan->h_soff.data(), plan->Mo, policy, param);
     std::unique_ptr<Schedule> hold(s);
     plan->free_schedule();
+    plan->tuned.clear();
     plan->sched = std::move(*s);
     if (plan->sched.policy != "row") {
       plan->d_group_off = upload(plan->sched.group_off);
@@ -983,6 +992,14 @@ int srbcrs_run_ex(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int
                   float* d_C, int64_t ldc, int64_t c_rows, const srbcrs_run_opts* opts,
                   void* stream) {
   return guarded([&] {
+    srbcrs_run_opts tuned_opts;
+    if (plan && (!opts || all_default(*opts))) {
+      const auto it = plan->tuned.find(N);
+      if (it != plan->tuned.end()) {
+        tuned_opts = it->second;
+        opts = &tuned_opts;
+      }
+    }
     srbcrs::RunOpts ro;
     int max_vec = 4;
     if (opts) {
@@ -1063,6 +1080,58 @@ int srbcrs_run_ex(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int
                           plan->d_rowmap};
     hip_check(srbcrs::launch_reduce(ra, vec, st), "launch segment_reduce");
   });
+}
+
+int srbcrs_plan_tune(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int64_t ldb, float* d_C,
+                     int64_t ldc, int64_t c_rows, int32_t reps, srbcrs_run_opts* best, void* stream) {
+  if (!plan) return guarded([] { fail(SRBCRS_EINVAL, "plan is NULL"); });
+  if (reps < 1 || reps > 100) return guarded([&] { fail(SRBCRS_EINVAL, "reps must be in [1, 100] (got %d)", reps); });
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  plan->tuned.erase(N);
+  std::vector<srbcrs_run_opts> cand;
+  for (int32_t a : {SRBCRS_A_COMPACT, SRBCRS_A_DENSE}) {
+    if (a == SRBCRS_A_COMPACT && !plan->d_awords) continue;
+    for (int32_t wg : {128, 64})
+      for (int32_t depth : {2, 4, 8}) {
+        srbcrs_run_opts o{};
+        o.depth = depth;
+        o.wg_cols = wg;
+        o.grid_order = SRBCRS_GRID_CHUNK_MAJOR;
+        o.a_operand = a;
+        cand.push_back(o);
+      }
+  }
+  hipEvent_t e0 = nullptr, e1 = nullptr;
+  int rc = guarded([&] {
+    hip_check(hipEventCreate(&e0), "hipEventCreate");
+    hip_check(hipEventCreate(&e1), "hipEventCreate");
+  });
+  float best_ms = -1.f;
+  srbcrs_run_opts best_o{};
+  for (size_t i = 0; rc == SRBCRS_OK && i < cand.size(); ++i) {
+    rc = srbcrs_run_ex(plan, d_B, K, N, ldb, d_C, ldc, c_rows, &cand[i], stream);   // warm-up, validates
+    if (rc != SRBCRS_OK) break;
+    rc = guarded([&] { hip_check(hipEventRecord(e0, st), "hipEventRecord"); });
+    for (int r = 0; rc == SRBCRS_OK && r < reps; ++r)
+      rc = srbcrs_run_ex(plan, d_B, K, N, ldb, d_C, ldc, c_rows, &cand[i], stream);
+    if (rc != SRBCRS_OK) break;
+    float ms = 0.f;
+    rc = guarded([&] {
+      hip_check(hipEventRecord(e1, st), "hipEventRecord");
+      hip_check(hipEventSynchronize(e1), "hipEventSynchronize");
+      hip_check(hipEventElapsedTime(&ms, e0, e1), "hipEventElapsedTime");
+    });
+    if (rc == SRBCRS_OK && (best_ms < 0.f || ms < best_ms)) {
+      best_ms = ms;
+      best_o = cand[i];
+    }
+  }
+  if (e0) (void)hipEventDestroy(e0);
+  if (e1) (void)hipEventDestroy(e1);
+  if (rc != SRBCRS_OK) return rc;
+  if (best_ms >= 0.f) plan->tuned[N] = best_o;
+  if (best) *best = best_o;
+  return SRBCRS_OK;
 }
 
 int srbcrs_csr_spmm(const int32_t* d_rowptr, const int32_t* d_colind, const float* d_values,

@@ -103,3 +103,41 @@ def test_compact_empty_matrix(gpu):
     _say("empty compact")
     c, d = _both(plan, t(np.ones((4, 32), np.float32)))
     assert not c.any() and not d.any()
+
+
+def test_tune_keeps_bits_and_sticks(gpu):
+    """srbcrs_plan_tune picks a setting; default-knob runs use it and give
+    the same bits as the untuned default; a schedule change drops it."""
+    import torch
+    from mask_amd.SRBCRSSpMM import Plan
+    rp, ci, vv = random_csr(700, 700, 0.01, 31, heavy_rows=2, heavy_len=600)
+    t = lambda a: torch.from_numpy(a).cuda()
+    plan = Plan(t(rp), t(ci), t(vv), 700)
+    for pol in (("row", 0), ("split", 0)):
+        plan.set_schedule(*pol)
+        for N in (64, 128):
+            B = t(np.random.default_rng(N).uniform(-1, 1, (700, N)).astype(np.float32))
+            _say("tune", pol, N)
+            ref = plan.run(B).clone()
+            C = torch.full_like(ref, float("nan"))
+            choice = plan.tune(B, C, reps=1)
+            assert choice["depth"] in (2, 4, 8) and choice["wg_cols"] in (64, 128)
+            assert choice["a_operand"] in ("compact", "dense")
+            assert torch.equal(C, ref)          # tune leaves the product in C
+            again = plan.run(B)
+            assert torch.equal(again, ref)
+            assert N in plan.tuned_widths
+    plan.set_schedule("row", 0)
+    assert not plan.tuned_widths
+
+
+def test_tune_rejects_bad_reps(gpu):
+    import torch
+    from mask_amd._capi import SrbcrsError
+    from mask_amd.SRBCRSSpMM import Plan
+    rp, ci, vv = random_csr(64, 64, 0.05, 1)
+    t = lambda a: torch.from_numpy(a).cuda()
+    plan = Plan(t(rp), t(ci), t(vv), 64)
+    B = t(np.ones((64, 32), np.float32))
+    with pytest.raises(SrbcrsError, match="reps"):
+        plan.tune(B, reps=0)
