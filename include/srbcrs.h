@@ -214,7 +214,9 @@ int srbcrs_run(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int64_
  *                (0 = 128);
  *   grid_order   0 = default (chunk-major), 1 = chunk-major: one column
  *                chunk of every window before the next chunk (narrower B
- *                working set per XCD), 2 = window-major;
+ *                working set per XCD), 2 = window-major, 3 = chunk sweep:
+ *                chunk-major in dispatch order, all XCDs on one chunk at a
+ *                time (its B rows shared through the memory-side cache);
  *   windows_per_wave  "row" schedule: consecutive row windows one wave
  *                streams through its register ring (0 = 1), in [0, 4096].
  * Values outside these sets are rejected.  Every setting yields the same
@@ -241,14 +243,16 @@ typedef struct srbcrs_run_opts {
 #define SRBCRS_GRID_DEFAULT 0
 #define SRBCRS_GRID_CHUNK_MAJOR 1
 #define SRBCRS_GRID_WINDOW_MAJOR 2
+#define SRBCRS_GRID_CHUNK_SWEEP 3
 
 /* srbcrs_run with explicit knobs (opts NULL = defaults). */
 int srbcrs_run_ex(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int64_t ldb,
                   float *d_C, int64_t ldc, int64_t c_rows, const srbcrs_run_opts *opts,
                   void *stream);
 
-/* Time the candidate launch settings (wg_cols 128 / 64 x depth 2 / 4 / 8,
- * chunk-major, x the compact and dense A operands) on this plan for a dense
+/* Time the candidate launch settings (grid order chunk-major / chunk sweep
+ * x wg_cols 128 / 64 x depth 2 / 4 x the compact and dense A operands:
+ * 16, or 8 without a compact copy) on this plan for a dense
  * width N, reps timed launches each after one warm-up, on `stream`, and
  * keep the fastest: later srbcrs_run calls, and srbcrs_run_ex calls whose
  * knobs are all 0, at that N use it until the schedule changes.  C is

@@ -116,7 +116,7 @@ class Plan:
             grid_order: int = 0, windows_per_wave: int = 0, a_operand: str = "default") -> Tensor:
         """out[:num_nodes] = A @ dense on the current stream.  The keyword
         knobs are the kernel template parameters (srbcrs_run_opts; 0 =
-        default; grid_order 1 = chunk-major, 2 = window-major; a_operand
+        default; grid_order 1 = chunk-major, 2 = window-major, 3 = chunk sweep; a_operand
         "compact" / "dense" picks the block-value copy the kernel reads)."""
         if out is None:
             out = torch.empty((self.num_nodes, dense.shape[1]), dtype=torch.float32, device=dense.device)

@@ -1009,11 +1009,13 @@ int srbcrs_run_ex(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int
         fail(SRBCRS_EINVAL, "tile_b must be 0, 16, 32 or 64 (got %d)", opts->tile_b);
       if (opts->wg_cols != 0 && (opts->wg_cols < 64 || opts->wg_cols > 512 || (opts->wg_cols & (opts->wg_cols - 1))))
         fail(SRBCRS_EINVAL, "wg_cols must be 0 or a power of two in [64, 512] (got %d)", opts->wg_cols);
-      if (opts->grid_order < 0 || opts->grid_order > 2)
-        fail(SRBCRS_EINVAL, "grid_order must be 0, 1 or 2 (got %d)", opts->grid_order);
+      if (opts->grid_order < 0 || opts->grid_order > 3)
+        fail(SRBCRS_EINVAL, "grid_order must be 0, 1, 2 or 3 (got %d)", opts->grid_order);
       if (opts->depth) ro.depth = opts->depth;
       if (opts->wg_cols) ro.wg_cols = opts->wg_cols;
-      if (opts->grid_order) ro.chunk_major = opts->grid_order == SRBCRS_GRID_CHUNK_MAJOR ? 1 : 0;
+      if (opts->grid_order)
+        ro.chunk_major = opts->grid_order == SRBCRS_GRID_CHUNK_MAJOR ? 1
+                         : opts->grid_order == SRBCRS_GRID_CHUNK_SWEEP ? 2 : 0;
       if (opts->windows_per_wave < 0 || opts->windows_per_wave > 4096)
         fail(SRBCRS_EINVAL, "windows_per_wave must be in [0, 4096] (got %d)", opts->windows_per_wave);
       ro.windows_per_wave = opts->windows_per_wave ? opts->windows_per_wave : 1;
@@ -1091,15 +1093,16 @@ int srbcrs_plan_tune(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
   std::vector<srbcrs_run_opts> cand;
   for (int32_t a : {SRBCRS_A_COMPACT, SRBCRS_A_DENSE}) {
     if (a == SRBCRS_A_COMPACT && !plan->d_awords) continue;
-    for (int32_t wg : {128, 64})
-      for (int32_t depth : {2, 4, 8}) {
-        srbcrs_run_opts o{};
-        o.depth = depth;
-        o.wg_cols = wg;
-        o.grid_order = SRBCRS_GRID_CHUNK_MAJOR;
-        o.a_operand = a;
-        cand.push_back(o);
-      }
+    for (int32_t order : {SRBCRS_GRID_CHUNK_MAJOR, SRBCRS_GRID_CHUNK_SWEEP})
+      for (int32_t wg : {128, 64})
+        for (int32_t depth : {2, 4}) {
+          srbcrs_run_opts o{};
+          o.depth = depth;
+          o.wg_cols = wg;
+          o.grid_order = order;
+          o.a_operand = a;
+          cand.push_back(o);
+        }
   }
   hipEvent_t e0 = nullptr, e1 = nullptr;
   int rc = guarded([&] {

@@ -11,7 +11,7 @@ namespace srbcrs {
 struct RunOpts {
   int depth = 2;             // units in flight per wave: 2, 4 or 8
   int wg_cols = 128;         // columns per workgroup (0 = up to 4 waves)
-  int chunk_major = 1;       // grid order: 0 window-major, 1 chunk-major
+  int chunk_major = 1;       // grid order: 0 window-major, 1 chunk-major, 2 chunk sweep (no XCD blocking)
   int windows_per_wave = 1;  // row schedule: consecutive windows streamed per wave
   int a_compact = 1;         // read A from the compact copy when the plan has one
 };

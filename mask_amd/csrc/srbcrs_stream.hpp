@@ -289,7 +289,7 @@ __device__ __forceinline__ void flush_task(const Src& src, int t, f4 (&acc)[BH /
 // n_chunks, in group-major order (all chunks of a group adjacent) or
 // chunk-major order (one column chunk of every group first: the B rows a
 // chunk touches are narrower, so neighbouring windows' shared rows stay in
-// L2).  Each wave streams the group's units through one DEPTH-deep register
+// L2), or chunk-major in plain dispatch order (below).  Each wave streams the group's units through one DEPTH-deep register
 // ring without draining it at task boundaries: the accumulator tile is
 // flushed and cleared when the unit index crosses a task's end.  Every
 // output element has exactly one writer per launch: no atomics.
@@ -306,7 +306,11 @@ __global__ __launch_bounds__(64 * WAVES) void spmm_stream(
   typedef Shape<BH, BW> S;
   constexpr int WCOLS = 16 * VEC * G;
   const int64_t nwg = (int64_t)gridDim.x;
-  const int64_t lid = xcd_remap(blockIdx.x, nwg);
+  // chunk_major 2: chunk-major in dispatch order (no XCD blocking), so every
+  // XCD sweeps the same column chunk at the same time and the chunk's B rows
+  // are shared through the memory-side cache instead of each XCD holding a
+  // different chunk.
+  const int64_t lid = chunk_major == 2 ? (int64_t)blockIdx.x : xcd_remap(blockIdx.x, nwg);
   const int64_t n_units = nwg / n_chunks;
   const int grp = (int)(chunk_major ? lid % n_units : lid / n_chunks);
   const int chunk = (int)(chunk_major ? lid / n_units : lid % n_chunks);

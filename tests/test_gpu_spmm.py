@@ -180,12 +180,12 @@ def test_knobs_are_bitwise_invariant(gpu):
     _say("knobs", M, K, N)
     ref, plan = _run_plan(rowptr, colind, values, M, B)
     dB = torch.from_numpy(B).cuda()
-    for depth, tile_b, wgc, go, wpw in itertools.product([2, 4, 8], [0, 16, 32], [0, 64, 256], [1, 2], [1, 3, 16]):
+    for depth, tile_b, wgc, go, wpw in itertools.product([2, 4, 8], [0, 16, 32], [0, 64, 256], [1, 2, 3], [1, 3, 16]):
         out = plan.run(dB, depth=depth, tile_b=tile_b, wg_cols=wgc, grid_order=go, windows_per_wave=wpw)
-        assert np.array_equal(out.cpu().numpy(), ref), (depth, tile_b, wgc, cm, wpw)
+        assert np.array_equal(out.cpu().numpy(), ref), (depth, tile_b, wgc, go, wpw)
     for pol in (("split", 0), ("strict_lb", 7), ("multi_bind", 0)):
         plan.set_schedule(*pol)
         base = plan.run(dB).cpu().numpy()
-        for depth, wgc, go in itertools.product([4, 8], [0, 64, 512], [1, 2]):
+        for depth, wgc, go in itertools.product([4, 8], [0, 64, 512], [1, 2, 3]):
             out = plan.run(dB, depth=depth, wg_cols=wgc, grid_order=go)
             assert np.array_equal(out.cpu().numpy(), base), (pol, depth, wgc, go)
