@@ -359,10 +359,33 @@ def cpu_baseline(m, B_host, N, budget_s):
             break
     t_med = float(np.median(times))
     nnz_s = int(rp[-1])
-    return {"value": round(2.0 * nnz_s * N / t_med / 1e9, 3), "unit": "GFLOP/s", "cores": cores, "kind": "port",
+    flops = 2.0 * nnz_s * N
+    # beside the baseline, on the same sample: the fp64 oracle (the checker, one run) and CPU
+    # torch.sparse.mm (the reference's torch fallback, external_backend_spmm.py:115-124)
+    t = time.perf_counter()
+    oracle.csr_spmm_f64(rp, ci, vv, B_host, rows.size)
+    t_f64 = time.perf_counter() - t
+    import torch
+    import warnings
+    with warnings.catch_warnings():
+        warnings.simplefilter("ignore")   # "sparse CSR support is in beta"
+        A = torch.sparse_csr_tensor(torch.from_numpy(rp.astype(np.int64)), torch.from_numpy(ci.astype(np.int64)),
+                                    torch.from_numpy(vv), size=(rows.size, B_host.shape[0]))
+    Bt = torch.from_numpy(B_host)
+    torch.sparse.mm(A, Bt)
+    tt = []
+    for _ in range(3):
+        t = time.perf_counter()
+        torch.sparse.mm(A, Bt)
+        tt.append(time.perf_counter() - t)
+    t_torch = float(np.median(tt))
+    return {"value": round(flops / t_med / 1e9, 3), "unit": "GFLOP/s", "cores": cores, "kind": "port",
             "sample": f"first {rows.size} rows ({nnz_s} nnz) of {m.name} at N={N}, median of {len(times)} runs, "
                       f"fp32 row-parallel CSR (oracle/srbcrs_oracle.c)",
-            "median_s": round(t_med, 5)}
+            "median_s": round(t_med, 5),
+            "oracle_f64_s": round(t_f64, 5),
+            "torch_sparse_cpu": {"value": round(flops / t_torch / 1e9, 3), "unit": "GFLOP/s",
+                                 "threads": torch.get_num_threads(), "median_s": round(t_torch, 5)}}
 
 
 if __name__ == "__main__":
