@@ -297,7 +297,8 @@ __device__ __forceinline__ void flush_task(const Src& src, int t, f4 (&acc)[BH /
 // Occupancy is left to the compiler: forcing 4 waves/SIMD on the default
 // instantiation (amdgpu_waves_per_eu, 98 registers instead of 146) made it
 // slower on the GPU (GCN N=256 1.83 -> 2.02 ms), because the tighter budget
-// delays the ring's loads.
+// delays the ring's loads.  With the compact A source (129 registers, 3
+// waves) forcing 4 waves is slower too (uniform 0.259 -> 0.274 ms).
 template <class Src, int BH, int BW, int VEC, int G, int WAVES, int DEPTH, class AF>
 __global__ __launch_bounds__(64 * WAVES) void spmm_stream(
     Src src, const float* __restrict__ B, float* __restrict__ C, float* __restrict__ partial,
