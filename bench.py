@@ -50,6 +50,8 @@ def parse():
     ap.add_argument("--wg-cols", type=int, default=0, help="kernel knob: columns per workgroup")
     ap.add_argument("--grid-order", type=int, default=0, help="kernel knob: 1 chunk-major, 2 window-major")
     ap.add_argument("--wpw", type=int, default=0, help="kernel knob: row windows streamed per wave")
+    ap.add_argument("--blk", default="16x8", choices=["16x8", "32x32"],
+                    help="SR-BCRS block shape (16x8: preprocess_gpu_16x8; 32x32: the base preprocess_gpu)")
     ap.add_argument("--no-tune", action="store_true",
                     help="skip srbcrs_plan_tune (the one-time launch-setting search run before the warm-up)")
     ap.add_argument("--a-operand", default="default", choices=["default", "compact", "dense"],
@@ -148,12 +150,13 @@ def a_operand_used(plan, requested):
     return "compact" if stored >= 0 and 2 * stored <= plan.total_blocks * plan.blk_h * plan.blk_w else "dense"
 
 
-def algorithmic_bytes(M, N, Mo, nb, nnz, kernel):
+def algorithmic_bytes(M, N, Mo, nb, nnz, kernel, bh=16, bw=8):
     """Dataflow bytes per launch.  SR-BCRS: metadata + A blocks + B rows
-    gathered per block + C written.  CSR: rowptr + (col, val) + B row per
+    gathered per block + C written (for 16x8 blocks: 4(Mo+1) + nb(8*4 +
+    128*4) + nb*8*N*4 + M*N*4).  CSR: rowptr + (col, val) + B row per
     nonzero + C."""
     if kernel == "srbcrs":
-        return 4 * (Mo + 1) + nb * (8 * 4 + 128 * 4) + nb * 8 * N * 4 + M * N * 4
+        return 4 * (Mo + 1) + nb * (bw * 4 + bh * bw * 4) + nb * bw * N * 4 + M * N * 4
     return 4 * (M + 1) + 8 * nnz + 4 * N * nnz + 4 * M * N
 
 
@@ -190,7 +193,8 @@ def main():
     C = torch.empty((m.M, N), dtype=torch.float32, device=dev)
 
     t0 = time.time()
-    plan = Plan(rowptr_d, colind_d, values_d, m.M, row_order=args.row_order, K=m.K)
+    bh, bw = (int(x) for x in args.blk.split("x"))
+    plan = Plan(rowptr_d, colind_d, values_d, m.M, bh, bw, row_order=args.row_order, K=m.K)
     conv_s = time.time() - t0
     nb, Mo = plan.total_blocks, plan.row_windows
     sched = args.schedule
@@ -239,11 +243,11 @@ def main():
         {"depth": args.depth or 2, "tile_b": args.tile_b, "wg_cols": args.wg_cols or 128,
          "grid_order": args.grid_order or 1, "windows_per_wave": args.wpw or 1,
          "a_operand": a_operand_used(plan, args.a_operand), "tuned": False}
-    ab = algorithmic_bytes(m.M, N, Mo, nb, m.nnz, args.kernel)
-    compulsory = (nb * (8 * 4 + 128 * 4) + 4 * (Mo + 1) if args.kernel == "srbcrs" else 8 * m.nnz) \
+    ab = algorithmic_bytes(m.M, N, Mo, nb, m.nnz, args.kernel, bh, bw)
+    compulsory = (nb * (bw * 4 + bh * bw * 4) + 4 * (Mo + 1) if args.kernel == "srbcrs" else 8 * m.nnz) \
         + m.K * N * 4 + m.M * N * 4
     achieved = ab / t_s / 1e9
-    padded_flops = 2.0 * 128 * nb * N
+    padded_flops = 2.0 * bh * bw * nb * N
 
     result = {
         "metric": "SpMM GFLOP/s at N=512 fp32 on 1 MI355X; % of HBM roofline",
@@ -260,7 +264,8 @@ def main():
         "dtype": "f32",
         "data": "synthetic (seeded numpy, see mask_amd/datasets.py)",
         "config": {"workload": m.name, "M": m.M, "K": m.K, "N": N, "nnz": m.nnz, "blocks": nb,
-                   "block_fill": round(m.nnz / (128 * max(nb, 1)), 4), "kernel": args.kernel,
+                   "block": args.blk, "block_fill": round(m.nnz / (bh * bw * max(nb, 1)), 4),
+                   "kernel": args.kernel,
                    "schedule": f"{plan.policy[0]}:{plan.policy[1]}", "seed": m.seed, "row_order": args.row_order,
                    "conversion_s": round(conv_s, 3), "meta": m.meta,
                    "knobs": knobs},
@@ -268,7 +273,8 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(m.name, N, args.kernel, knobs
                                                  if args.schedule == "auto" and not args.tile_b and not args.wpw
-                                                 and args.row_order == "identity" and not args.mtx else None),
+                                                 and args.row_order == "identity" and not args.mtx
+                                                 and args.blk == "16x8" else None),
                      "algorithmic_bytes": int(ab), "compulsory_bytes": int(compulsory),
                      "compulsory_frac": round(compulsory / t_s / 1e9 / HBM_PEAK_GBS, 4),
                      "mfma_padded_tflops": round(padded_flops / t_s / 1e12, 3),
