@@ -35,6 +35,8 @@ def parse():
                     choices=["uniform-4096", "uniform-65536", "banded-524288", "rmat-2^20", "gcn-232965"])
     ap.add_argument("--N", type=int, default=None, help="dense width (default: the workload's)")
     ap.add_argument("--mtx", default=None, help="a MatrixMarket file instead of a synthetic workload")
+    ap.add_argument("--gcn-train", action="store_true",
+                    help="GCN training step (ReplaceableGCN 512-256-64 + Adam) through the srbcrs_spmm drop-in")
     ap.add_argument("--gcn-forward", action="store_true",
                     help="time the GCN workload's two-layer forward instead of one SpMM")
     ap.add_argument("--row-order", default="identity",
@@ -136,6 +138,68 @@ def gcn_forward_bench(args):
     }), flush=True)
 
 
+def gcn_train_bench(args):
+    """Full-batch GCN training steps on the GCN workload through the drop-in
+    path the reference's GCN script uses (eva_gcn_sparsene.py:267-343):
+    ReplaceableGCN(512, 256, 64, 2 layers, dropout 0.5) with the
+    srbcrs_spmm external backend (forward A @ X, backward A^T @ dY on the
+    transposed CSR), log-softmax + NLL on synthetic labels, Adam.  Timed per
+    SR-BCRS variant (16x8 and the 32x32 base) and, for comparison, with the
+    torch backend (torch.sparse.mm on ROCm).  One JSON line."""
+    import torch
+    import torch.nn.functional as F
+    from mask_amd import datasets
+    from mask_amd.external_backend_spmm import reset_backend_state, srbcrs_spmm
+    from mask_amd.gcn import ReplaceableGCN, SpMMBackend, graph_from_csr
+    dev = torch.device("cuda", 0)
+    m = datasets.make_config("gcn-232965")
+    data = graph_from_csr(m, 512, dev, seed=m.seed)
+    labels = torch.randint(0, 64, (m.M,), generator=torch.Generator().manual_seed(m.seed)).to(dev)
+    if not args.no_tune:
+        os.environ["SPARSENE_SRBCRS_AUTOTUNE"] = "1"   # tuned on each plan's first call per width
+    results, losses = {}, {}
+    for name in ("16x8", "base", "torch"):
+        os.environ["SPARSENE_SRBCRS_VARIANT"] = "16x8" if name == "torch" else name
+        reset_backend_state()
+        backend = SpMMBackend("torch") if name == "torch" else SpMMBackend("external:srbcrs_spmm", srbcrs_spmm)
+        torch.manual_seed(m.seed)
+        model = ReplaceableGCN(512, 256, 64, 2, 0.5).to(dev)
+        opt = torch.optim.Adam(model.parameters(), lr=0.01)
+
+        def step():
+            opt.zero_grad(set_to_none=True)
+            loss = F.nll_loss(model(data, backend), labels)
+            loss.backward()
+            opt.step()
+            return loss
+
+        t0 = time.time()
+        step()   # conversion of A and A^T (and tuning) happens here, outside the timed steps
+        torch.cuda.synchronize()
+        setup_s = time.time() - t0
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        e[0].record()
+        for _ in range(args.steps):
+            loss = step()
+        e[1].record()
+        torch.cuda.synchronize()
+        results[name] = {"ms_per_step": round(e[0].elapsed_time(e[1]) / args.steps, 4),
+                         "first_step_s": round(setup_s, 3)}
+        losses[name] = round(float(loss), 5)
+    print(json.dumps({
+        "metric": "GCN training step time (gcn-232965, ReplaceableGCN 512-256-64, Adam, full batch)",
+        "value": results["16x8"]["ms_per_step"], "unit": "ms", "higher_is_better": False, "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "dtype": "f32",
+        "data": "synthetic R-MAT graph, N(0,1) features, uniform labels (seeded)",
+        "config": {"workload": m.name, "nodes": m.M, "nnz": m.nnz, "spmm": "srbcrs_spmm drop-in",
+                   "autotune": not args.no_tune},
+        "variants": results, "final_loss": losses,
+    }), flush=True)
+
+
 def tuned_knobs(t, tune_s):
     return {"depth": t["depth"], "tile_b": 0, "wg_cols": t["wg_cols"], "grid_order": t["grid_order"],
             "windows_per_wave": 1, "a_operand": t["a_operand"], "tuned": True, "tune_s": round(tune_s, 3)}
@@ -169,6 +233,9 @@ def main():
 
     if args.copy_calibration_mb:
         copy_calibration(args.copy_calibration_mb)
+        return
+    if args.gcn_train:
+        gcn_train_bench(args)
         return
     if args.gcn_forward:
         gcn_forward_bench(args)

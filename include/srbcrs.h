@@ -169,7 +169,10 @@ int srbcrs_plan_row_order(const srbcrs_plan *plan, int32_t *order, int32_t capac
  *                fragmenting of strict_load_balance
  *                (main_strict_lb_16x8.cu:208-256, CFE:719-749);
  *   "multi_bind" windows above 2x the mean split into ceil(x/mean) parts
- *                (main_multi_bind_16x8.cu:211-270, CFE:750-780).
+ *                (main_multi_bind_16x8.cu:211-270, CFE:750-780);
+ *   "auto"       "split" (param 0) when the longest window exceeds
+ *                max(64, 4 x the 95th-percentile window), else "row" (the
+ *                split rule's own heavy-tail test; param ignored).
  * Partial windows go to private partial tiles that a deterministic segment
  * reduction (fixed slot order) sums into C: no atomics anywhere, unlike
  * the reference's atomicAdd edges (kernel_lb.inc:9-58).

@@ -23,7 +23,7 @@ from . import _capi
 
 Tensor = torch.Tensor
 
-_POLICIES = ("row", "split", "strict_lb", "multi_bind")
+_POLICIES = ("row", "split", "strict_lb", "multi_bind", "auto")
 
 
 def _check_input(t: Tensor, name: str) -> None:
@@ -308,7 +308,8 @@ def _run(dense: Tensor, row_window_offset: Tensor, tcblocktile_id: Tensor, tcblo
     if entry.plan.total_blocks <= 0:
         raise RuntimeError("SR-BCRS has empty preprocessed blocks; CSR fallback disabled.")
     sched = _schedule_from_exeplan(exeplan)
-    entry.plan.set_schedule(*(sched or ("row", 0)))
+    # no schedule requested: "auto" (split on heavy-tailed windows, else one task per window)
+    entry.plan.set_schedule(*(sched or ("auto", 0)))
     out = torch.empty((entry.num_nodes, n), dtype=torch.float32, device=dense.device)
     if os.environ.get("SPARSENE_SRBCRS_AUTOTUNE", "0") == "1" and n not in entry.plan.tuned_widths:
         entry.plan.tune(dense, out)   # once per (width, schedule); the product lands in out

@@ -250,6 +250,23 @@ void push_task(Schedule& s, int32_t b, int32_t e, int32_t w) {
   s.task_slot.push_back(-1);
 }
 
+// Longest window and the 95th-percentile window length, in blocks.
+void window_stats(const int32_t* soff, int32_t Mo, int32_t& mx, int32_t& p95) {
+  std::vector<int32_t> len(Mo);
+  mx = 0;
+  for (int32_t w = 0; w < Mo; ++w) {
+    len[w] = soff[w + 1] - soff[w];
+    mx = std::max(mx, len[w]);
+  }
+  p95 = 0;
+  if (Mo > 0) {
+    std::sort(len.begin(), len.end());
+    int64_t i = (int64_t)std::ceil(Mo * 0.95) - 1;
+    i = std::min<int64_t>(std::max<int64_t>(i, 0), Mo - 1);
+    p95 = len[i];
+  }
+}
+
 Schedule* build_schedule(const int32_t* soff, int32_t Mo, const char* policy_c, int32_t param) {
   if (!soff) fail(SRBCRS_EINVAL, "soff is NULL");
   if (Mo < 0) fail(SRBCRS_EINVAL, "row_windows must be >= 0");
@@ -258,6 +275,14 @@ Schedule* build_schedule(const int32_t* soff, int32_t Mo, const char* policy_c, 
   std::string policy = policy_c ? policy_c : "row";
   if (policy.empty()) policy = "row";
   if (param < 0) fail(SRBCRS_EINVAL, "schedule parameter must be >= 0");
+  if (policy == "auto") {
+    // split when the block counts have a heavy tail (the split policy's own
+    // test: longest window > max(64, 4 * p95)), else one task per window
+    int32_t mx, p95;
+    window_stats(soff, Mo, mx, p95);
+    policy = mx > std::max(64, 4 * std::max(p95, 1)) ? "split" : "row";
+    param = 0;
+  }
   auto* s = new Schedule();
   s->policy = policy;
   s->param = param;
@@ -273,19 +298,8 @@ Schedule* build_schedule(const int32_t* soff, int32_t Mo, const char* policy_c, 
       if (param > 0) {
         cap = param;
       } else {
-        std::vector<int32_t> len(Mo);
-        int32_t mx = 0;
-        for (int32_t w = 0; w < Mo; ++w) {
-          len[w] = soff[w + 1] - soff[w];
-          mx = std::max(mx, len[w]);
-        }
-        int32_t p95 = 0;
-        if (Mo > 0) {
-          std::sort(len.begin(), len.end());
-          int64_t i = (int64_t)std::ceil(Mo * 0.95) - 1;
-          i = std::min<int64_t>(std::max<int64_t>(i, 0), Mo - 1);
-          p95 = len[i];
-        }
+        int32_t mx, p95;
+        window_stats(soff, Mo, mx, p95);
         const int32_t p = std::max(p95, 1);
         const bool heavy = mx > std::max(64, 4 * p);
         cap = heavy ? std::max(32, std::min(128, 2 * p95)) : std::max(mx, 1);
@@ -345,7 +359,7 @@ Schedule* build_schedule(const int32_t* soff, int32_t Mo, const char* policy_c, 
         }
       }
     } else {
-      fail(SRBCRS_EINVAL, "unknown schedule policy '%s' (row, split, strict_lb, multi_bind)",
+      fail(SRBCRS_EINVAL, "unknown schedule policy '%s' (row, split, strict_lb, multi_bind, auto)",
            policy.c_str());
     }
     assign_slots(*s, Mo);

@@ -164,6 +164,22 @@ def test_row_schedule_and_errors():
         _capi.build_schedule(np.array([0, 5, 2], np.int32), "row")
 
 
+def test_auto_schedule_picks_split_on_heavy_tail_else_row():
+    """"auto" = the split rule's heavy-tail test: longest window > max(64,
+    4 x p95) -> the split:0 tables; otherwise the row tables."""
+    flat = np.cumsum([0] + [5] * 40 + [60]).astype(np.int32)          # longest 60 <= 64
+    assert _same_tables(_capi.build_schedule(flat, "auto")) == _same_tables(_capi.build_schedule(flat, "row"))
+    heavy = np.cumsum([0] + [5] * 40 + [300]).astype(np.int32)        # 300 > max(64, 20)
+    a, b = _capi.build_schedule(heavy, "auto"), _capi.build_schedule(heavy, "split")
+    assert _same_tables(a) == _same_tables(b) and a["n_slots"] > 0
+    ratio = np.cumsum([0] + [20] * 40 + [79]).astype(np.int32)         # 79 <= 4 x 20
+    assert _same_tables(_capi.build_schedule(ratio, "auto")) == _same_tables(_capi.build_schedule(ratio, "row"))
+
+
+def _same_tables(s):
+    return {k: (v.tolist() if isinstance(v, np.ndarray) else v) for k, v in s.items()}
+
+
 # ---- drop-in module argument checks (no GPU needed to reach them) ------------------
 
 def test_dropin_rejects_host_tensors():
