@@ -263,6 +263,7 @@ int srbcrs_run_ex(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int
  * tuning changes only the time.  best (may be NULL) receives the choice.
  * No reference counterpart: the reference fixes its launch shape at build
  * time (strategy_agent.py:81-130 picks it offline). */
+/* Not thread-safe against a concurrent srbcrs_run* on the same plan. */
 int srbcrs_plan_tune(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int64_t ldb,
                      float *d_C, int64_t ldc, int64_t c_rows, int32_t reps, srbcrs_run_opts *best,
                      void *stream);
