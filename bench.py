@@ -349,11 +349,13 @@ def main():
         "wall_s_timed": round(wall, 4),
     }
 
-    if not args.no_check:
-        result["parity"] = check_sample(m, B_host, C.cpu().numpy(), N)
-
-    if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(m, B_host, N, args.cpu_seconds)
+    if not (args.no_check and args.no_cpu):
+        parity, base = cpu_baseline_leg(m, B_host, N, args.cpu_seconds, None if args.no_check else C.cpu().numpy(),
+                                        time_baseline=not args.no_cpu)
+        if parity is not None:
+            result["parity"] = parity
+        if base is not None:
+            result["cpu_baseline"] = base
 
     print(json.dumps(result), flush=True)
 
@@ -398,9 +400,8 @@ def _row_sample(m, rows):
     return sub_rp.astype(np.int32), m.colind[idx], m.values[idx]
 
 
-def check_sample(m, B_host, C, N, n_rows=4096):
+def _check_sample(oracle, m, B_host, C, n_rows=4096):
     """Correctness gate on a seeded row sample against the fp64 oracle."""
-    from oracle import oracle
     rng = np.random.default_rng(0)
     rows = np.sort(rng.choice(m.M, size=min(n_rows, m.M), replace=False))
     rp, ci, vv = _row_sample(m, rows)
@@ -411,10 +412,19 @@ def check_sample(m, B_host, C, N, n_rows=4096):
     return met
 
 
-def cpu_baseline(m, B_host, N, budget_s):
+def cpu_baseline_leg(m, B_host, N, budget_s, C=None, time_baseline=True):
+    """The CPU leg: the only place bench.py touches oracle/.  Returns
+    (parity, cpu_baseline): the fp64 oracle as the checker of the GPU result
+    C on a seeded row sample (None when C is None), and the timed CPU
+    baseline (None unless time_baseline)."""
+    from oracle import oracle
+    parity = _check_sample(oracle, m, B_host, C) if C is not None else None
+    return parity, (cpu_baseline(oracle, m, B_host, N, budget_s) if time_baseline else None)
+
+
+def cpu_baseline(oracle, m, B_host, N, budget_s):
     """The oracle's fp32 CSR SpMM (csr_spmm_value_kernel's arithmetic) on the
     host cores over a bounded row sample, repeated within the time budget."""
-    from oracle import oracle
     cores = len(os.sched_getaffinity(0))
     # sample sized for ~1 s per repetition at ~1 GFLOP/s per core
     target_flops = 1e9 * cores
