@@ -202,7 +202,8 @@ def gcn_train_bench(args):
 
 def tuned_knobs(t, tune_s):
     return {"depth": t["depth"], "tile_b": 0, "wg_cols": t["wg_cols"], "grid_order": t["grid_order"],
-            "windows_per_wave": 1, "a_operand": t["a_operand"], "tuned": True, "tune_s": round(tune_s, 3)}
+            "windows_per_wave": t["windows_per_wave"], "a_operand": t["a_operand"], "tuned": True,
+            "tune_s": round(tune_s, 3)}
 
 
 def a_operand_used(plan, requested):
@@ -339,7 +340,7 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": measured_traffic(m.name, N, args.kernel, knobs
-                                                 if args.schedule == "auto" and not args.tile_b and not args.wpw
+                                                 if args.schedule == "auto" and not args.tile_b
                                                  and args.row_order == "identity" and not args.mtx
                                                  and args.blk == "16x8" else None),
                      "algorithmic_bytes": int(ab), "compulsory_bytes": int(compulsory),
@@ -377,7 +378,8 @@ def measured_traffic(workload, N, kernel, knobs):
             traffic = int(line.split(":", 1)[1])
         elif line.startswith("knobs:"):
             prof_knobs = dict(kv.split("=") for kv in line.split(":", 1)[1].split())
-    want = {k: str(knobs[k]) for k in ("depth", "wg_cols", "grid_order", "a_operand")}
+    want = {k: str(knobs[k]) for k in ("depth", "wg_cols", "grid_order", "windows_per_wave", "a_operand")}
+    prof_knobs = prof_knobs and {"windows_per_wave": "1", **prof_knobs}
     return traffic if prof_knobs == want else None
 
 

@@ -254,8 +254,9 @@ int srbcrs_run_ex(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int
                   void *stream);
 
 /* Time the candidate launch settings (grid order chunk-major / chunk sweep
- * x wg_cols 128 / 64 x depth 2 / 4 x the compact and dense A operands:
- * 16, or 8 without a compact copy) on this plan for a dense
+ * x wg_cols 128 / 64 x depth 2 / 4, plus, on the "row" schedule, 4 / 8
+ * windows per wave x depth 4 / 8; each for the compact and the dense A
+ * operand when the plan has a compact copy) on this plan for a dense
  * width N, reps timed launches each after one warm-up, on `stream`, and
  * keep the fastest: later srbcrs_run calls, and srbcrs_run_ex calls whose
  * knobs are all 0, at that N use it until the schedule changes.  C is

@@ -153,7 +153,7 @@ class Plan:
         self.tuned_widths.add(int(dense.shape[1]))
         inv = {v: k for k, v in _capi.A_OPERANDS.items()}
         return {"depth": best.depth, "wg_cols": best.wg_cols, "grid_order": best.grid_order,
-                "a_operand": inv[best.a_operand]}
+                "windows_per_wave": best.windows_per_wave or 1, "a_operand": inv[best.a_operand]}
 
     def row_order(self):
         """The plan's row order (new -> original) as a numpy array."""
