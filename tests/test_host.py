@@ -318,3 +318,13 @@ def test_packing_rejects_bad_options():
         _capi.pack_host(rp, ci, vv, 20, 5)
     with pytest.raises(_capi.SrbcrsError, match="square"):
         _capi.row_order_host(rp, ci, 20, 30, "row_rcm")
+
+
+def test_header_is_c99_and_c_client_builds(tmp_path):
+    """include/srbcrs.h compiles as C99 (no C++ in the ABI) and a plain C
+    client links against the library."""
+    import subprocess
+    from tests.c_client import ROOT, compile_client
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-fsyntax-only", "-x", "c",
+                    str(ROOT / "include" / "srbcrs.h")], check=True)
+    assert compile_client(tmp_path / "client").exists()
