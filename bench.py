@@ -358,6 +358,11 @@ def main():
         if base is not None:
             result["cpu_baseline"] = base
 
+    tr = result["roofline"].get("traffic")
+    if tr:
+        # measured L2-miss bytes per launch over the same step time: how close the memory side runs
+        # to the HBM peak (the algorithmic fraction above counts cache-served re-reads too)
+        result["roofline"]["traffic_frac"] = round(tr / t_s / 1e9 / HBM_PEAK_GBS, 4)
     print(json.dumps(result), flush=True)
 
 
