@@ -35,6 +35,8 @@ def parse():
                     choices=["uniform-4096", "uniform-65536", "banded-524288", "rmat-2^20", "gcn-232965"])
     ap.add_argument("--N", type=int, default=None, help="dense width (default: the workload's)")
     ap.add_argument("--mtx", default=None, help="a MatrixMarket file instead of a synthetic workload")
+    ap.add_argument("--shard-sim", type=int, default=0,
+                    help="time one GPU's share of a G-way row sharding and column sharding (one GPU, no communication)")
     ap.add_argument("--gcn-train", action="store_true",
                     help="GCN training step (ReplaceableGCN 512-256-64 + Adam) through the srbcrs_spmm drop-in")
     ap.add_argument("--gcn-forward", action="store_true",
@@ -138,6 +140,76 @@ def gcn_forward_bench(args):
     }), flush=True)
 
 
+def _time_ms(fn, steps, warmup):
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    e[0].record()
+    for _ in range(steps):
+        fn()
+    e[1].record()
+    torch.cuda.synchronize()
+    return e[0].elapsed_time(e[1]) / steps
+
+
+def shard_sim_bench(args):
+    """One GPU's share of a G-way sharding of the workload, timed at its real
+    shape on this GPU (communication excluded, one JSON line):
+      rows:    srbcrs_shard_windows cuts the row windows into G ranges of
+               near-equal cost; every shard's plan is tuned and timed; the
+               critical path is the slowest shard;
+      columns: every GPU holds all of A and N/G columns of B and C: the full
+               plan at width N/G."""
+    import torch
+    from mask_amd import datasets
+    from mask_amd.SRBCRSSpMM import Plan
+    from mask_amd.sharding import RowShardedSpMM
+    dev = torch.device("cuda", 0)
+    G = args.shard_sim
+    m = datasets.make_config(args.config)
+    N = args.N or m.N
+    t = lambda a: torch.from_numpy(a).to(dev)
+    rp, ci, vv = t(m.rowptr), t(m.colind), t(m.values)
+    B = t(m.dense(N))
+    C = torch.empty((m.M, N), device=dev)
+    sh = RowShardedSpMM(rp, ci, vv, m.M, G)
+    sh.set_schedule("auto")
+    row_ms = []
+    for i, (r0, r1) in enumerate(sh.ranges):
+        if sh.plans[i] is None:
+            row_ms.append(0.0)
+            continue
+        sh.plans[i].tune(B, C[r0:r1])
+        row_ms.append(_time_ms(lambda: sh.run_shard(i, B, C), args.steps, args.warmup))
+    full = Plan(rp, ci, vv, m.M)
+    full.set_schedule("auto")
+    Nc = N // G if N % (16 * G) == 0 else 0
+    col_ms = None
+    if Nc:
+        Bc = B[:, :Nc].contiguous()
+        Cc = torch.empty((m.M, Nc), device=dev)
+        full.tune(Bc, Cc)
+        col_ms = _time_ms(lambda: full.run(Bc, Cc), args.steps, args.warmup)
+    full.tune(B, C)
+    one_ms = _time_ms(lambda: full.run(B, C), args.steps, args.warmup)
+    flops = 2.0 * m.nnz * N
+    mx = max(row_ms)
+    print(json.dumps({
+        "metric": f"simulated {G}-way sharding of the SpMM: one GPU's share timed on one MI355X (no communication)",
+        "value": round(flops / mx / 1e6, 1), "unit": "GFLOP/s (row sharding, critical path)",
+        "higher_is_better": True, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "dtype": "f32",
+        "config": {"workload": m.name, "N": N, "shards": G},
+        "one_gpu_ms": round(one_ms, 4),
+        "rows": {"ranges": sh.ranges, "shard_ms": [round(x, 4) for x in row_ms], "max_ms": round(mx, 4),
+                 "imbalance": round(mx / (sum(row_ms) / G), 3), "speedup_vs_one": round(one_ms / mx, 2)},
+        "columns": None if col_ms is None else {
+            "N_per_gpu": Nc, "ms": round(col_ms, 4), "speedup_vs_one": round(one_ms / col_ms, 2),
+            "gflops": round(flops / col_ms / 1e6, 1)},
+    }), flush=True)
+
+
 def gcn_train_bench(args):
     """Full-batch GCN training steps on the GCN workload through the drop-in
     path the reference's GCN script uses (eva_gcn_sparsene.py:267-343):
@@ -237,6 +309,9 @@ def main():
         return
     if args.gcn_train:
         gcn_train_bench(args)
+        return
+    if args.shard_sim > 1:
+        shard_sim_bench(args)
         return
     if args.gcn_forward:
         gcn_forward_bench(args)

@@ -269,6 +269,15 @@ int srbcrs_plan_tune(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, 
                      float *d_C, int64_t ldc, int64_t c_rows, int32_t reps, srbcrs_run_opts *best,
                      void *stream);
 
+/* ---- Sharding over GPUs (design support; this build runs on one GPU).
+ * Cut the row windows into n_shards contiguous ranges of near-equal cost
+ * (blocks + one output tile per window): shard s owns windows
+ * [bounds[s], bounds[s+1]), i.e. rows [16 * bounds[s], 16 * bounds[s+1])
+ * for 16-row windows, and writes its C rows with no reduction.  bounds has
+ * n_shards + 1 entries.  No reference counterpart (the reference is
+ * single-GPU). */
+int srbcrs_shard_windows(const int32_t *soff, int32_t row_windows, int32_t n_shards, int32_t *bounds);
+
 /* ---- CSR fallback for low block density: C[r, :] = sum_e val[e] *
  * B[col[e], :], fp32, edge order.  The arithmetic of csr_spmm_value_kernel
  * (SRK:66-105), one wave64 per row.  max_col (host-known bound on colind,

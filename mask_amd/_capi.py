@@ -28,7 +28,7 @@ EXPORTS = (
     "srbcrs_schedule_build", "srbcrs_schedule_info", "srbcrs_schedule_export", "srbcrs_schedule_destroy",
     "srbcrs_plan_set_schedule", "srbcrs_run", "srbcrs_run_ex", "srbcrs_csr_spmm",
     "srbcrs_row_order", "srbcrs_pack_count", "srbcrs_pack_fill", "srbcrs_plan_create_ex", "srbcrs_plan_row_order",
-    "srbcrs_plan_tune",
+    "srbcrs_plan_tune", "srbcrs_shard_windows",
 )
 
 _i32p = ctypes.POINTER(ctypes.c_int32)
@@ -127,6 +127,7 @@ def lib() -> ctypes.CDLL:
         "srbcrs_plan_create_ex": ([_vp, _vp, _vp, _i32, _i64, ctypes.POINTER(PackOpts), _i32, _vp,
                                    ctypes.POINTER(_vp)], ctypes.c_int),
         "srbcrs_plan_row_order": ([_vp, _vp, _i32, _i32p], ctypes.c_int),
+        "srbcrs_shard_windows": ([_vp, _i32, _i32, _vp], ctypes.c_int),
         "srbcrs_plan_tune": ([_vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i32, ctypes.POINTER(RunOpts), _vp],
                              ctypes.c_int),
         "srbcrs_csr_spmm": ([_vp, _vp, _vp, _i32, _i64, _i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp],
@@ -179,6 +180,14 @@ def convert_host(rowptr, colind, values, num_nodes: int, blk_h: int = 16, blk_w:
                                 ptr(sidx), ptr(val), ptr(bp), ptr(e2r), ptr(e2c)))
     return dict(soff=soff, sidx=sidx[: t * blk_w], val=val[: t * blk_h * blk_w], block_partition=bp[:mo],
                 edge_to_row=e2r[:nnz], edge_to_col=e2c[:nnz], total=t)
+
+
+def shard_windows(soff, n_shards: int) -> np.ndarray:
+    """Balanced contiguous window ranges (see srbcrs_shard_windows)."""
+    soff = np.ascontiguousarray(soff, dtype=np.int32)
+    bounds = np.zeros(int(n_shards) + 1, np.int32)
+    check(lib().srbcrs_shard_windows(ptr(soff), soff.shape[0] - 1, int(n_shards), ptr(bounds)))
+    return bounds
 
 
 def build_schedule(soff, policy: str, param: int = 0) -> dict:

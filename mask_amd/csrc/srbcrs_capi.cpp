@@ -1164,6 +1164,28 @@ int srbcrs_plan_tune(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
   return SRBCRS_OK;
 }
 
+int srbcrs_shard_windows(const int32_t* soff, int32_t row_windows, int32_t n_shards, int32_t* bounds) {
+  return guarded([&] {
+    if (!soff || !bounds) fail(SRBCRS_EINVAL, "soff / bounds is NULL");
+    if (row_windows < 0) fail(SRBCRS_EINVAL, "row_windows must be >= 0");
+    if (n_shards < 1) fail(SRBCRS_EINVAL, "n_shards must be >= 1");
+    for (int32_t w = 0; w < row_windows; ++w)
+      if (soff[w + 1] < soff[w]) fail(SRBCRS_EINVAL, "soff must be non-decreasing");
+    // cost of a window = its blocks + 1 (the output tile it writes): shard s
+    // ends at the first window boundary whose prefix cost reaches
+    // (s+1)/n_shards of the total
+    const int64_t total = (int64_t)(soff[row_windows] - soff[0]) + row_windows;
+    bounds[0] = 0;
+    int32_t w = 0;
+    for (int32_t sh = 1; sh < n_shards; ++sh) {
+      const int64_t target = (total * sh + n_shards - 1) / n_shards;
+      while (w < row_windows && (int64_t)(soff[w] - soff[0]) + w < target) ++w;
+      bounds[sh] = w;
+    }
+    bounds[n_shards] = row_windows;
+  });
+}
+
 int srbcrs_csr_spmm(const int32_t* d_rowptr, const int32_t* d_colind, const float* d_values,
                     int32_t M, int64_t nnz, int32_t max_col, const float* d_B, int64_t K, int64_t N,
                     int64_t ldb, float* d_C, int64_t ldc, void* stream) {

@@ -328,3 +328,30 @@ def test_header_is_c99_and_c_client_builds(tmp_path):
     subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-fsyntax-only", "-x", "c",
                     str(ROOT / "include" / "srbcrs.h")], check=True)
     assert compile_client(tmp_path / "client").exists()
+
+
+@pytest.mark.parametrize("n_shards", [1, 2, 3, 8, 50])
+def test_shard_windows_balanced_and_contiguous(n_shards):
+    """Contiguous cover of the windows; each shard's cost (blocks + 1 per
+    window) stays within one window of the ideal share; the cut points are
+    the first windows whose prefix cost reaches s/n of the total."""
+    rng = np.random.default_rng(n_shards)
+    lens = rng.integers(0, 40, size=37)
+    lens[5] = 300                                  # one heavy window
+    soff = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    b = _capi.shard_windows(soff, n_shards)
+    assert b[0] == 0 and b[-1] == lens.size and (np.diff(b) >= 0).all()
+    cost = np.concatenate([[0], np.cumsum(lens + 1)])
+    total = int(cost[-1])
+    for s in range(1, n_shards):
+        target = -(-total * s // n_shards)
+        assert b[s] == int(np.searchsorted(cost, target, side="left"))   # first prefix cost >= target
+    shard_cost = cost[b[1:]] - cost[b[:-1]]
+    assert shard_cost.max() <= total / n_shards + (lens.max() + 1)
+
+
+def test_shard_windows_rejects_bad_input():
+    with pytest.raises(_capi.SrbcrsError, match="n_shards"):
+        _capi.shard_windows(np.array([0, 1], np.int32), 0)
+    with pytest.raises(_capi.SrbcrsError, match="non-decreasing"):
+        _capi.shard_windows(np.array([0, 5, 2], np.int32), 2)
