@@ -444,23 +444,22 @@ def main():
 def measured_traffic(workload, N, kernel, knobs):
     """HBM bytes per launch of the dominant kernel from the committed
     rocprofv3 PMC summary (FETCH_SIZE and WRITE_SIZE runs, scaled by the
-    copy-kernel calibration), when one exists for this workload and was
-    profiled with the launch settings this run used (its "knobs:" line);
-    None otherwise."""
+    copy-kernel calibration), from the profile of this workload whose
+    "knobs:" line matches the launch settings this run used; None if there
+    is none."""
     if kernel != "srbcrs" or knobs is None:
         return None
-    path = ROOT / "profiles" / f"spmm_stream_{workload.replace('^', '')}_N{N}.md"
-    if not path.exists():
-        return None
-    traffic, prof_knobs = None, None
-    for line in path.read_text().splitlines():
-        if line.startswith("traffic_bytes:"):
-            traffic = int(line.split(":", 1)[1])
-        elif line.startswith("knobs:"):
-            prof_knobs = dict(kv.split("=") for kv in line.split(":", 1)[1].split())
     want = {k: str(knobs[k]) for k in ("depth", "wg_cols", "grid_order", "windows_per_wave", "a_operand")}
-    prof_knobs = prof_knobs and {"windows_per_wave": "1", **prof_knobs}
-    return traffic if prof_knobs == want else None
+    for path in sorted((ROOT / "profiles").glob(f"spmm_stream_{workload.replace('^', '')}_N{N}*.md")):
+        traffic, prof_knobs = None, None
+        for line in path.read_text().splitlines():
+            if line.startswith("traffic_bytes:"):
+                traffic = int(line.split(":", 1)[1])
+            elif line.startswith("knobs:"):
+                prof_knobs = dict(kv.split("=") for kv in line.split(":", 1)[1].split())
+        if prof_knobs and {"windows_per_wave": "1", **prof_knobs} == want:
+            return traffic
+    return None
 
 
 def datasets_soff(plan):

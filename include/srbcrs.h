@@ -253,18 +253,19 @@ int srbcrs_run_ex(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int
                   float *d_C, int64_t ldc, int64_t c_rows, const srbcrs_run_opts *opts,
                   void *stream);
 
-/* Time the candidate launch settings (grid order chunk-major / chunk sweep
- * x wg_cols 128 / 64 x depth 2 / 4, plus, on the "row" schedule, 4 / 8
- * windows per wave x depth 4 / 8; each for the compact and the dense A
- * operand when the plan has a compact copy) on this plan for a dense
- * width N, reps timed launches each after one warm-up, on `stream`, and
- * keep the fastest: later srbcrs_run calls, and srbcrs_run_ex calls whose
- * knobs are all 0, at that N use it until the schedule changes.  C is
- * overwritten (with the product).  Every candidate gives the same bits, so
- * tuning changes only the time.  best (may be NULL) receives the choice.
- * No reference counterpart: the reference fixes its launch shape at build
- * time (strategy_agent.py:81-130 picks it offline). */
-/* Not thread-safe against a concurrent srbcrs_run* on the same plan. */
+/* Time candidate launch settings on this plan for a dense width N and keep
+ * one.  Candidates, in preference order: for the compact A operand (when
+ * the plan has the copy), then for the dense one: grid order chunk-major /
+ * chunk sweep x wg_cols 128 / 64 x depth 2 / 4, then, on the "row"
+ * schedule, 4 / 8 windows per wave x depth 4 / 8.  Each gets one warm-up
+ * and `reps` timed launches on `stream`; the first candidate within 3 % of
+ * the fastest wins, so near-ties resolve the same way on every run.  Later
+ * srbcrs_run calls, and srbcrs_run_ex calls whose knobs are all 0, use it
+ * at that N until the schedule changes.  C is overwritten (with the
+ * product).  Every candidate gives the same bits: tuning changes only the
+ * time.  best (may be NULL) receives the choice.  Not thread-safe against a
+ * concurrent srbcrs_run* on the same plan.  No reference counterpart: the
+ * reference fixes its launch shape offline (strategy_agent.py:81-130). */
 int srbcrs_plan_tune(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int64_t ldb,
                      float *d_C, int64_t ldc, int64_t c_rows, int32_t reps, srbcrs_run_opts *best,
                      void *stream);
