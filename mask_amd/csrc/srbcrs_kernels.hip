@@ -41,18 +41,20 @@ hipError_t launch_reduce(const ReduceArgs& a, int vec, hipStream_t st) {
 
 // vec: columns per lane per pass (64*vec divides N, or 1).
 hipError_t launch_csr(const CsrArgs& a, int vec, hipStream_t st) {
-  const int64_t nwg = ((int64_t)a.M + 3) / 4;
+  const int n_chunks = (a.N + 64 * vec - 1) / (64 * vec);
+  const int64_t nwg = ((int64_t)a.M + 3) / 4 * n_chunks;
   if (nwg == 0) return hipSuccess;
+  if (nwg > INT32_MAX) return hipErrorInvalidConfiguration;
   dim3 grid((unsigned)nwg);
   if (vec == 4)
-    hipLaunchKernelGGL((csr_spmm_rowwave<4, 4>), grid, dim3(256), 0, st, a.rowptr, a.colind,
-                       a.values, a.B, a.C, a.M, a.N, a.ldb, a.ldc);
+    hipLaunchKernelGGL((csr_spmm_rowwave<4, 8>), grid, dim3(256), 0, st, a.rowptr, a.colind,
+                       a.values, a.B, a.C, a.M, a.N, a.ldb, a.ldc, n_chunks);
   else if (vec == 2)
-    hipLaunchKernelGGL((csr_spmm_rowwave<2, 4>), grid, dim3(256), 0, st, a.rowptr, a.colind,
-                       a.values, a.B, a.C, a.M, a.N, a.ldb, a.ldc);
+    hipLaunchKernelGGL((csr_spmm_rowwave<2, 8>), grid, dim3(256), 0, st, a.rowptr, a.colind,
+                       a.values, a.B, a.C, a.M, a.N, a.ldb, a.ldc, n_chunks);
   else
-    hipLaunchKernelGGL((csr_spmm_rowwave<1, 4>), grid, dim3(256), 0, st, a.rowptr, a.colind,
-                       a.values, a.B, a.C, a.M, a.N, a.ldb, a.ldc);
+    hipLaunchKernelGGL((csr_spmm_rowwave<1, 8>), grid, dim3(256), 0, st, a.rowptr, a.colind,
+                       a.values, a.B, a.C, a.M, a.N, a.ldb, a.ldc, n_chunks);
   return hipGetLastError();
 }
 

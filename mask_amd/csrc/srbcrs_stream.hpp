@@ -429,44 +429,49 @@ __global__ __launch_bounds__(256) void zero_rows(T* __restrict__ C, const int* _
   }
 }
 
-// CSR SpMM, one wave per row: lane owns VEC consecutive columns per
-// 64*VEC-column pass.  Edge-ordered fp32 accumulation, the arithmetic of the
-// reference's csr_spmm_value_kernel (examples/src_fp32/sr_bcrs/testbed/
-// SRBCRSSpMM_kernel.cu:66-87), laid out for wave64 vector loads.
+// CSR SpMM, one wave per (row, column chunk): lane owns VEC consecutive
+// columns of a 64*VEC-column chunk.  Edge-ordered fp32 accumulation, the
+// arithmetic of the reference's csr_spmm_value_kernel (examples/src_fp32/
+// sr_bcrs/testbed/SRBCRSSpMM_kernel.cu:66-87), laid out for wave64 vector
+// loads.  The grid is chunk-major (every row's first chunk before any second
+// chunk), which keeps the B columns in flight narrow: 17-22 % faster than
+// looping over the chunks inside the wave on the uniform and R-MAT
+// workloads.  UNROLL B rows are loaded before their FMAs.
 template <int VEC, int UNROLL>
 __global__ __launch_bounds__(256) void csr_spmm_rowwave(
     const int* __restrict__ rowptr, const int* __restrict__ colind,
     const float* __restrict__ values, const float* __restrict__ B, float* __restrict__ C, int M,
-    int N, int64_t ldb, int64_t ldc) {
+    int N, int64_t ldb, int64_t ldc, int n_chunks) {
   typedef typename VecT<VEC>::type V;
   const int64_t nwg = (int64_t)gridDim.x;
   const int64_t lid = xcd_remap(blockIdx.x, nwg);
-  const int64_t row = lid * 4 + (threadIdx.x >> 6);
+  const int64_t row_groups = nwg / n_chunks;
+  const int chunk = (int)(lid / row_groups);
+  const int64_t row = (lid % row_groups) * 4 + (threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  if (row >= M) return;
+  const int c = chunk * 64 * VEC + VEC * lane;
+  if (row >= M || c >= N) return;
   const int e0 = rowptr[row], e1 = rowptr[row + 1];
-  for (int c = VEC * lane; c < N; c += 64 * VEC) {
-    V acc;
-    if constexpr (VEC == 1) acc = 0.f; else { for (int s = 0; s < VEC; ++s) acc[s] = 0.f; }
-    int e = e0;
-    for (; e + UNROLL <= e1; e += UNROLL) {
-      V bv[UNROLL];
-      float av[UNROLL];
+  V acc;
+  if constexpr (VEC == 1) acc = 0.f; else { for (int s = 0; s < VEC; ++s) acc[s] = 0.f; }
+  int e = e0;
+  for (; e + UNROLL <= e1; e += UNROLL) {
+    V bv[UNROLL];
+    float av[UNROLL];
 #pragma unroll
-      for (int u = 0; u < UNROLL; ++u) {
-        const int col = colind[e + u];
-        av[u] = values[e + u];
-        bv[u] = *reinterpret_cast<const V*>(B + (int64_t)col * ldb + c);
-      }
+    for (int u = 0; u < UNROLL; ++u) {
+      const int col = colind[e + u];
+      av[u] = values[e + u];
+      bv[u] = *reinterpret_cast<const V*>(B + (int64_t)col * ldb + c);
+    }
 #pragma unroll
-      for (int u = 0; u < UNROLL; ++u) acc += av[u] * bv[u];
-    }
-    for (; e < e1; ++e) {
-      const int col = colind[e];
-      acc += values[e] * *reinterpret_cast<const V*>(B + (int64_t)col * ldb + c);
-    }
-    *reinterpret_cast<V*>(C + row * ldc + c) = acc;
+    for (int u = 0; u < UNROLL; ++u) acc += av[u] * bv[u];
   }
+  for (; e < e1; ++e) {
+    const int col = colind[e];
+    acc += values[e] * *reinterpret_cast<const V*>(B + (int64_t)col * ldb + c);
+  }
+  *reinterpret_cast<V*>(C + row * ldc + c) = acc;
 }
 
 }  // namespace srbcrs
