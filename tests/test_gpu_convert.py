@@ -90,3 +90,37 @@ def test_device_conversion_rejects_malformed(gpu):
         Plan(t(np.array([0, 9], np.int32)), t(np.array([0, 1], np.int32)), t(np.ones(2, np.float32)), 1)
     with pytest.raises(SrbcrsError, match="negative"):
         Plan(t(np.array([0, 2], np.int32)), t(np.array([1, -4], np.int32)), t(np.ones(2, np.float32)), 1)
+
+
+@pytest.mark.parametrize("name", ["convert_16x8_hand.json", "convert_32x32_hand.json"])
+def test_device_conversion_matches_golden(gpu, name):
+    """The device converter against the hand-derived fixtures."""
+    import torch
+    from mask_amd.SRBCRSSpMM import Plan
+    from tests.test_golden import arrays, load
+    g = load(name)
+    rp, ci, vv = arrays(g)
+    t = lambda a: torch.from_numpy(a).cuda()
+    _say("golden", name)
+    got = _arrays(Plan(t(rp), t(ci), t(vv), g["num_nodes"], *g["blk"]))
+    assert got["total"] == g["total"]
+    for k in ("soff", "sidx", "block_partition", "edge_to_row", "edge_to_col"):
+        assert got[k].tolist() == g[k], k
+    assert got["val"].tobytes() == np.asarray(g["val"], np.float32).tobytes()
+
+
+@pytest.mark.parametrize("a_operand", ["compact", "dense"])
+@pytest.mark.parametrize("blk", [(16, 8), (32, 32)])
+def test_spmm_exact_golden(gpu, blk, a_operand):
+    """Power-of-two A times small-integer B: every sum is exact in fp32, so
+    C must equal the fixture bit for bit."""
+    import torch
+    from mask_amd.SRBCRSSpMM import Plan
+    from tests.test_golden import arrays, load
+    g = load("spmm_exact.json")
+    rp, ci, vv = arrays(g)
+    t = lambda a: torch.from_numpy(a).cuda()
+    _say("exact spmm", blk, a_operand)
+    plan = Plan(t(rp), t(ci), t(vv), g["num_nodes"], *blk)
+    C = plan.run(t(np.asarray(g["B"], np.float32)), a_operand=a_operand).cpu().numpy()
+    assert np.array_equal(C, np.asarray(g["C"], np.float32))
