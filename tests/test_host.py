@@ -355,3 +355,29 @@ def test_shard_windows_rejects_bad_input():
         _capi.shard_windows(np.array([0, 1], np.int32), 0)
     with pytest.raises(_capi.SrbcrsError, match="non-decreasing"):
         _capi.shard_windows(np.array([0, 5, 2], np.int32), 2)
+
+
+def test_bench_byte_model_and_traffic_lookup():
+    """bench.py's algorithmic-bytes formula (SR-BCRS dataflow: metadata, A
+    blocks, gathered B rows, C) and its profile lookup by launch settings."""
+    import sys
+    sys.argv = ["bench.py"]
+    import bench
+    M, N, Mo, nb = 65536, 512, 4096, 131072
+    assert bench.algorithmic_bytes(M, N, Mo, nb, 0, "srbcrs") == \
+        4 * (Mo + 1) + nb * (8 * 4 + 128 * 4) + nb * 8 * N * 4 + M * N * 4
+    assert bench.algorithmic_bytes(M, N, Mo, nb // 8, 0, "srbcrs", 32, 32) == \
+        4 * (Mo + 1) + nb // 8 * (32 * 4 + 1024 * 4) + nb // 8 * 32 * N * 4 + M * N * 4
+    assert bench.algorithmic_bytes(10, 64, 1, 1, 100, "csr") == 4 * 11 + 8 * 100 + 4 * 64 * 100 + 4 * 10 * 64
+    from pathlib import Path
+    prof = sorted((Path(bench.ROOT) / "profiles").glob("spmm_stream_uniform-65536_N512_*.md"))
+    assert prof, "no committed uniform profile"
+    knobs = None
+    for line in prof[0].read_text().splitlines():
+        if line.startswith("knobs:"):
+            knobs = dict(kv.split("=") for kv in line.split(":", 1)[1].split())
+    assert knobs is not None
+    got = bench.measured_traffic("uniform-65536", 512, "srbcrs", knobs)
+    assert isinstance(got, int) and got > 0
+    assert bench.measured_traffic("uniform-65536", 512, "srbcrs", {**knobs, "depth": "3"}) is None
+    assert bench.measured_traffic("uniform-65536", 512, "csr", knobs) is None
