@@ -360,8 +360,6 @@ def test_shard_windows_rejects_bad_input():
 def test_bench_byte_model_and_traffic_lookup():
     """bench.py's algorithmic-bytes formula (SR-BCRS dataflow: metadata, A
     blocks, gathered B rows, C) and its profile lookup by launch settings."""
-    import sys
-    sys.argv = ["bench.py"]
     import bench
     M, N, Mo, nb = 65536, 512, 4096, 131072
     assert bench.algorithmic_bytes(M, N, Mo, nb, 0, "srbcrs") == \
