@@ -255,7 +255,9 @@ int srbcrs_run_ex(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int
 
 /* Time candidate launch settings on this plan for a dense width N and keep
  * one.  Candidates, in preference order: for the compact A operand (when
- * the plan has the copy), then for the dense one: grid order chunk-major /
+ * the plan has the copy and at most 3/4 of the block positions hold
+ * values), then for the dense one (unless under 1/4 hold values and the
+ * compact copy exists): grid order chunk-major /
  * chunk sweep x wg_cols 128 / 64 x depth 2 / 4, then, on the "row"
  * schedule, 4 / 8 windows per wave x depth 4 / 8.  Each gets one warm-up
  * and `reps` timed launches on `stream`; the first candidate within 3 % of
