@@ -28,36 +28,45 @@ int grid_for(int64_t n) {
   return (int)(g < 1 ? 1 : (g > 65536 ? 65536 : g));
 }
 
-// One thread per word: its mask and the number of stored values.
-__global__ void k_word_masks(const float* __restrict__ val, int64_t n_words, int words_per_block,
-                             int block_size, uint2* __restrict__ words, uint32_t* __restrict__ counts) {
-  for (int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; w < n_words;
-       w += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t blk = w / words_per_block;
-    const int j = (int)(w % words_per_block);
-    const float* vb = val + blk * block_size;
-    uint32_t m = 0;
-    for (int t = 0; t < 32; ++t)
-      if (__float_as_uint(vb[swz(32 * j + t)]) != 0u) m |= 1u << t;
-    words[w] = make_uint2(m, 0u);
-    counts[w] = (uint32_t)__builtin_popcount(m);
+// One thread per logical block position.  The swizzle only permutes offset
+// bits 2..3, so the 32 positions of a word lie in one 128-byte span of val
+// and a wave's reads coalesce; a wave ballot gives the masks of its two
+// words.  Grid-stride steps are multiples of 64 positions, so every wave
+// stays whole for the ballot (the position count is a multiple of 64).
+__global__ void k_word_masks(const float* __restrict__ val, int64_t n_pos, int block_size,
+                             uint2* __restrict__ words, uint32_t* __restrict__ counts) {
+  const int lane = threadIdx.x & 63;
+  for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < n_pos;
+       g += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t blk = g / block_size;
+    const int p = (int)(g % block_size);
+    const bool stored = __float_as_uint(val[blk * block_size + swz(p)]) != 0u;
+    const uint64_t bal = __ballot(stored);
+    if ((lane & 31) == 0) {
+      const uint32_t m = (uint32_t)(bal >> (lane & 32));
+      const int64_t w = g >> 5;
+      words[w] = make_uint2(m, 0u);
+      counts[w] = (uint32_t)__builtin_popcount(m);
+    }
   }
 }
 
-// One thread per word: the base offset and the packed values.
-__global__ void k_word_fill(const float* __restrict__ val, int64_t n_words, int words_per_block,
-                            int block_size, const uint32_t* __restrict__ bases, uint2* __restrict__ words,
+// One thread per logical block position: the word's base offset and the
+// packed value of every stored position.
+__global__ void k_word_fill(const float* __restrict__ val, int64_t n_pos, int block_size,
+                            const uint32_t* __restrict__ bases, uint2* __restrict__ words,
                             float* __restrict__ packed) {
-  for (int64_t w = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; w < n_words;
-       w += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t blk = w / words_per_block;
-    const int j = (int)(w % words_per_block);
-    const float* vb = val + blk * block_size;
-    const uint32_t m = words[w].x, base = bases[w];
-    words[w].y = base;
-    uint32_t n = base;
-    for (int t = 0; t < 32; ++t)
-      if ((m >> t) & 1u) packed[n++] = vb[swz(32 * j + t)];
+  for (int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; g < n_pos;
+       g += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t w = g >> 5;
+    const int t = (int)(g & 31);
+    uint32_t* wd = reinterpret_cast<uint32_t*>(words);   // [2w] = mask (read), [2w+1] = base (written)
+    const uint32_t m = wd[2 * w], base = bases[w];
+    if ((m >> t) & 1u) {
+      const int64_t blk = g / block_size;
+      packed[base + __builtin_popcount(m & ((1u << t) - 1u))] = val[blk * block_size + swz((int)(g % block_size))];
+    }
+    if (t == 0) wd[2 * w + 1] = base;
   }
 }
 
@@ -98,8 +107,9 @@ hipError_t device_compact(const float* val, int64_t n_blocks, int blk_h, int blk
   bases = (uint32_t*)alloc(ctx, (size_t)n_words * 4);
   tail = (uint32_t*)alloc(ctx, 8);
   if (!out.words || !counts || !bases || !tail) return fail(hipErrorOutOfMemory);
-  hipLaunchKernelGGL(k_word_masks, dim3(grid_for(n_words)), dim3(256), 0, st, val, n_words, wpb, block_size,
-                     out.words, counts);
+  const int64_t n_pos = n_words * 32;
+  hipLaunchKernelGGL(k_word_masks, dim3(grid_for(n_pos)), dim3(256), 0, st, val, n_pos, block_size, out.words,
+                     counts);
   SRBCRS_STEP(hipGetLastError());
   size_t bytes = 0;
   SRBCRS_STEP(hipcub::DeviceScan::ExclusiveSum(nullptr, bytes, counts, bases, (int)n_words, st));
@@ -114,8 +124,8 @@ hipError_t device_compact(const float* val, int64_t n_blocks, int blk_h, int blk
   out.n_packed = (int64_t)h_tail[0] + h_tail[1];
   out.packed = (float*)alloc(ctx, (size_t)(out.n_packed > 0 ? out.n_packed : 1) * 4);
   if (!out.packed) return fail(hipErrorOutOfMemory);
-  hipLaunchKernelGGL(k_word_fill, dim3(grid_for(n_words)), dim3(256), 0, st, val, n_words, wpb, block_size,
-                     bases, out.words, out.packed);
+  hipLaunchKernelGGL(k_word_fill, dim3(grid_for(n_pos)), dim3(256), 0, st, val, n_pos, block_size, bases,
+                     out.words, out.packed);
   SRBCRS_STEP(hipGetLastError());
   SRBCRS_STEP(hipStreamSynchronize(st));
 #undef SRBCRS_STEP

@@ -36,10 +36,14 @@ __global__ void k_validate_rowptr(const int* __restrict__ rowptr, int num_nodes,
   }
 }
 
-__global__ void k_row_ids(const int* __restrict__ rowptr, int num_nodes, int* __restrict__ e2r) {
+// Row ids of the edges in two parallel passes (a per-row loop serialises on
+// hub rows): each non-empty row marks its first edge (one writer per edge:
+// rows with the same start are empty but the last), then an inclusive max
+// scan over the zero-filled edge range carries each mark forward.
+__global__ void k_row_starts(const int* __restrict__ rowptr, int num_nodes, int* __restrict__ e2r) {
   for (int64_t r = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; r < num_nodes;
        r += (int64_t)gridDim.x * blockDim.x)
-    for (int e = rowptr[r]; e < rowptr[r + 1]; ++e) e2r[e] = (int)r;
+    if (rowptr[r + 1] > rowptr[r]) e2r[rowptr[r]] = (int)r;
 }
 
 __global__ void k_make_keys(const int* __restrict__ colind, const int* __restrict__ e2r, int e0,
@@ -198,8 +202,30 @@ hipError_t device_convert(const DeviceConvertIn& in, DeviceConvertOut& out, Devi
   // 2. row ids (also edge_to_row), keys
   int* e2r = in.edge_to_row;
   SRBCRS_TRY(hipGetLastError());
-  hipLaunchKernelGGL(k_row_ids, dim3(grid_for(in.num_nodes)), dim3(256), 0, st, in.rowptr, in.num_nodes, e2r);
+  hipLaunchKernelGGL(k_row_starts, dim3(grid_for(in.num_nodes)), dim3(256), 0, st, in.rowptr, in.num_nodes, e2r);
   SRBCRS_TRY(hipGetLastError());
+  if (n > 0) {   // carry the marks over [e0, e0 + n) (the caller zero-filled edge_to_row)
+    int* scanned = (int*)alloc(ctx, (size_t)n * 4);
+    void* scan_tmp = nullptr;
+    size_t scan_bytes = 0;
+    hipError_t e = scanned ? hipSuccess : hipErrorOutOfMemory;
+    if (e == hipSuccess)
+      e = hipcub::DeviceScan::InclusiveScan(nullptr, scan_bytes, e2r + e0, scanned, hipcub::Max(), n, st);
+    if (e == hipSuccess) {
+      scan_tmp = alloc(ctx, scan_bytes ? scan_bytes : 1);
+      if (!scan_tmp) e = hipErrorOutOfMemory;
+    }
+    if (e == hipSuccess)
+      e = hipcub::DeviceScan::InclusiveScan(scan_tmp, scan_bytes, e2r + e0, scanned, hipcub::Max(), n, st);
+    if (e == hipSuccess) e = hipMemcpyAsync(e2r + e0, scanned, (size_t)n * 4, hipMemcpyDeviceToDevice, st);
+    if (e == hipSuccess) e = hipStreamSynchronize(st);
+    if (scanned) dfree(ctx, scanned);
+    if (scan_tmp) dfree(ctx, scan_tmp);
+    if (e != hipSuccess) {
+      dfree(ctx, d_flag);
+      return e;
+    }
+  }
   uint64_t *k0 = nullptr, *k1 = nullptr;
   int *i0 = nullptr, *i1 = nullptr, *flags = nullptr, *rank = nullptr;
   int *ucol = nullptr, *uwin = nullptr, *ufirst = nullptr, *nb = nullptr;
