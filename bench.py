@@ -280,11 +280,13 @@ def tuned_knobs(t, tune_s):
 
 def a_operand_used(plan, requested):
     """The block-value copy the SR-BCRS kernel reads (mirrors the library's
-    default: compact when at most half of the block positions are stored)."""
+    default: for 16x8 blocks compact when at most half of the block positions
+    are stored; 32x32 blocks read the dense array)."""
     if requested != "default":
         return requested
     stored = plan.desc.stored_values
-    return "compact" if stored >= 0 and 2 * stored <= plan.total_blocks * plan.blk_h * plan.blk_w else "dense"
+    sparse = stored >= 0 and 2 * stored <= plan.total_blocks * plan.blk_h * plan.blk_w
+    return "compact" if sparse and plan.blk_h == 16 else "dense"
 
 
 def algorithmic_bytes(M, N, Mo, nb, nnz, kernel, bh=16, bw=8):

@@ -214,7 +214,9 @@ int srbcrs_run(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int64_
  *                MFMA sweep (16 * vector width) (0 = widest legal); the
  *                reference's N tile (SRBCRSSpMM_kernel.cu:435-475);
  *   wg_cols      columns per workgroup, a power of two in 64..512
- *                (0 = 128);
+ *                (0 = 128); 32x32 blocks run 128-column waves (two
+ *                64-column groups per lane) in workgroups of 256 columns
+ *                or more, 64-column waves below;
  *   grid_order   0 = default (chunk-major), 1 = chunk-major: one column
  *                chunk of every window before the next chunk (narrower B
  *                working set per XCD), 2 = window-major, 3 = chunk sweep:
@@ -236,9 +238,10 @@ typedef struct srbcrs_run_opts {
 /* a_operand: where the kernel reads the block values from.  Both give the
  * same bits.  COMPACT reads the plan's compact copy (per 32 block positions
  * a {mask, base} word plus the stored values; built at plan creation); DENSE
- * reads the reference-layout value array.  DEFAULT = COMPACT when the plan
- * has the copy (it is skipped when it would not fit) and at most half of the
- * block positions hold values, else DENSE. */
+ * reads the reference-layout value array.  DEFAULT = COMPACT for 16x8
+ * blocks when the plan has the copy (it is skipped when it would not fit)
+ * and at most half of the block positions hold values, else DENSE (always
+ * DENSE for 32x32 blocks). */
 #define SRBCRS_A_DEFAULT 0
 #define SRBCRS_A_COMPACT 1
 #define SRBCRS_A_DENSE 2
@@ -254,11 +257,12 @@ int srbcrs_run_ex(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int
                   void *stream);
 
 /* Time candidate launch settings on this plan for a dense width N and keep
- * one.  Candidates, in preference order: for the compact A operand (when
- * the plan has the copy and at most 3/4 of the block positions hold
- * values), then for the dense one (unless under 1/4 hold values and the
- * compact copy exists): grid order chunk-major /
- * chunk sweep x wg_cols 128 / 64 x depth 2 / 4, then, on the "row"
+ * one.  Candidates, in preference order: for the compact A operand (16x8
+ * blocks, when the plan has the copy and at most 3/4 of the block positions
+ * hold values), then for the dense one (unless, for 16x8, under 1/4 hold
+ * values and the compact copy exists): grid order chunk-major /
+ * chunk sweep x wg_cols 128 / 64 (/ 256 for 32x32 blocks) x depth 2 / 4,
+ * then, on the "row"
  * schedule, 4 / 8 windows per wave x depth 4 / 8.  Each gets one warm-up
  * and `reps` timed launches on `stream`; the first candidate within 3 % of
  * the fastest wins, so near-ties resolve the same way on every run.  Later

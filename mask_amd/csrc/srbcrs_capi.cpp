@@ -1041,12 +1041,15 @@ int srbcrs_run_ex(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int
     if (opts && opts->a_operand == SRBCRS_A_COMPACT && !plan->d_awords && plan->total > 0)
       fail(SRBCRS_ESTATE, "the plan has no compact copy of its block values");
     {
-      // default: the compact copy when at most half of the block positions
-      // hold values (it skips the zeros; at full blocks it only adds the
-      // mask words and the decode: banded, fill 1.0, runs 13 % slower on it)
+      // default: for 16x8 blocks, the compact copy when at most half of the
+      // block positions hold values (it skips the zeros; at full blocks it
+      // only adds the mask words and the decode: banded, fill 1.0, runs 13 %
+      // slower on it).  32x32 blocks read the dense array: their two 16-row
+      // halves decode separate words for one B fragment, and compact lost on
+      // every workload measured (uniform 0.42 vs 0.38 ms at 3 % fill)
       const int a_op = opts ? opts->a_operand : SRBCRS_A_DEFAULT;
       const bool sparse_blocks = 2 * plan->n_apacked <= plan->total * (int64_t)plan->blk_h * plan->blk_w;
-      ro.a_compact = a_op == SRBCRS_A_COMPACT || (a_op == SRBCRS_A_DEFAULT && sparse_blocks);
+      ro.a_compact = a_op == SRBCRS_A_COMPACT || (a_op == SRBCRS_A_DEFAULT && sparse_blocks && plan->blk_h == 16);
     }
     int cur = 0;
     hip_check(hipGetDevice(&cur), "hipGetDevice");
@@ -1108,14 +1111,17 @@ int srbcrs_plan_tune(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
   // block fill decides the A source outright at the extremes (measured: compact wins by 14-20 %
   // at 6 % fill, dense by 13 % at 100 %), so only the middle band times both
   const int64_t positions = plan->total * (int64_t)plan->blk_h * plan->blk_w;
-  const bool mostly_empty = plan->d_awords && 4 * plan->n_apacked < positions;
+  // (16x8; 32x32 blocks time only the dense source, see srbcrs_run_ex)
+  const bool wide = plan->blk_h == 32;
+  const bool mostly_empty = !wide && plan->d_awords && 4 * plan->n_apacked < positions;
   const bool mostly_full = 4 * plan->n_apacked > 3 * positions;
   for (int32_t a : {SRBCRS_A_COMPACT, SRBCRS_A_DENSE}) {
-    if (a == SRBCRS_A_COMPACT && (!plan->d_awords || mostly_full)) continue;
+    if (a == SRBCRS_A_COMPACT && (!plan->d_awords || mostly_full || wide)) continue;
     if (a == SRBCRS_A_DENSE && mostly_empty) continue;
     for (int32_t order : {SRBCRS_GRID_CHUNK_MAJOR, SRBCRS_GRID_CHUNK_SWEEP})
-      for (int32_t wg : {128, 64})
+      for (int32_t wg : {128, 64, 256})
         for (int32_t depth : {2, 4}) {
+          if (wg == 256 && plan->blk_h != 32) continue;   // 32x32 only: two 128-column waves
           srbcrs_run_opts o{};
           o.depth = depth;
           o.wg_cols = wg;

@@ -44,13 +44,18 @@ static hipError_t launch_vg(const Src& src, const AF& af, int n_groups, const St
 // vec (4, 2 or 1; 16*vec divides N) is chosen by the caller from N, the
 // leading dimensions and pointer alignment.  16x8: G = 2 column groups per
 // wave when the 128-column wave tile divides N and wider-than-64 workgroups
-// are allowed.  32x32 (four units and two row halves per block) keeps G = 1
-// to bound the register ring.
+// are allowed.  32x32 (four units and two row halves per block) runs G = 2
+// only in workgroups of 256 columns or more: it halves the A loads per MFMA
+// (banded, full blocks: 0.72 -> 0.61 ms) but its register ring leaves 2
+// waves per SIMD, and at 3 % block fill (uniform, GCN, R-MAT) two 64-column
+// waves of G = 1 in a 128-column workgroup are faster (0.38 vs 0.42 ms).
 template <class AF, class Src, int DEPTH>
 static hipError_t launch_d(const Src& src, const AF& af, int n_groups, const StreamArgs& a, int vec,
                            const RunOpts& o, hipStream_t st) {
   if (a.blk_h == 32) {
-    if (vec == 4) return launch_vg<AF, Src, 32, 32, 4, 1, DEPTH>(src, af, n_groups, a, o, st);
+    if (vec == 4)
+      return (a.N % 128 == 0 && o.wg_cols >= 256) ? launch_vg<AF, Src, 32, 32, 4, 2, DEPTH>(src, af, n_groups, a, o, st)
+                                                 : launch_vg<AF, Src, 32, 32, 4, 1, DEPTH>(src, af, n_groups, a, o, st);
     if (vec == 2) return launch_vg<AF, Src, 32, 32, 2, 1, DEPTH>(src, af, n_groups, a, o, st);
     return launch_vg<AF, Src, 32, 32, 1, 1, DEPTH>(src, af, n_groups, a, o, st);
   }

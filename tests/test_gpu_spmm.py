@@ -19,12 +19,12 @@ def _torch():
     return torch
 
 
-def _run_plan(rowptr, colind, values, M, B, policy=("row", 0), device=None):
+def _run_plan(rowptr, colind, values, M, B, policy=("row", 0), device=None, blk=(16, 8)):
     torch = _torch()
     from mask_amd.SRBCRSSpMM import Plan
     dev = device or torch.device("cuda", 0)
     plan = Plan(torch.from_numpy(rowptr).to(dev), torch.from_numpy(colind).to(dev), torch.from_numpy(values).to(dev),
-                M)
+                M, blk[0], blk[1])
     plan.set_schedule(*policy)
     dB = torch.from_numpy(B).to(dev)
     out = plan.run(dB)
@@ -168,17 +168,19 @@ def test_csr_fallback(gpu):
         assert_gate(gate(out.cpu().numpy(), rowptr, colind, values, B, M))
 
 
-def test_knobs_are_bitwise_invariant(gpu):
+@pytest.mark.parametrize("blk", [(16, 8), (32, 32)])
+def test_knobs_are_bitwise_invariant(gpu, blk):
     """Depth, tile_b, workgroup width, grid order and windows-per-wave change
     only the mapping, never the per-element accumulation order: every
-    combination reproduces the default result bit for bit."""
+    combination reproduces the default result bit for bit (for 32x32
+    blocks, wg_cols 256 and 512 select the 128-column waves)."""
     torch = _torch()
     import itertools
     M, K, N = 333, 900, 256
     rowptr, colind, values = random_csr(M, K, 0.02, seed=31, empty_rows=0.3, heavy_rows=3, heavy_len=400)
     B = np.random.default_rng(4).uniform(-1, 1, (K, N)).astype(np.float32)
-    _say("knobs", M, K, N)
-    ref, plan = _run_plan(rowptr, colind, values, M, B)
+    _say("knobs", blk, M, K, N)
+    ref, plan = _run_plan(rowptr, colind, values, M, B, blk=blk)
     dB = torch.from_numpy(B).cuda()
     for depth, tile_b, wgc, go, wpw in itertools.product([2, 4, 8], [0, 16, 32], [0, 64, 256], [1, 2, 3], [1, 3, 16]):
         out = plan.run(dB, depth=depth, tile_b=tile_b, wg_cols=wgc, grid_order=go, windows_per_wave=wpw)

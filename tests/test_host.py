@@ -379,3 +379,20 @@ def test_bench_byte_model_and_traffic_lookup():
     assert isinstance(got, int) and got > 0
     assert bench.measured_traffic("uniform-65536", 512, "srbcrs", {**knobs, "depth": "3"}) is None
     assert bench.measured_traffic("uniform-65536", 512, "csr", knobs) is None
+
+
+def test_bench_reports_the_library_default_a_operand():
+    """bench.a_operand_used mirrors srbcrs_run_ex's default A source: compact
+    for sparse 16x8 plans, dense for full 16x8 plans and for any 32x32 plan."""
+    import types
+    import bench
+
+    def plan(bh, bw, stored, blocks):
+        return types.SimpleNamespace(blk_h=bh, blk_w=bw, total_blocks=blocks,
+                                     desc=types.SimpleNamespace(stored_values=stored))
+
+    assert bench.a_operand_used(plan(16, 8, 10, 4), "default") == "compact"     # 10 of 512 positions
+    assert bench.a_operand_used(plan(16, 8, 400, 4), "default") == "dense"
+    assert bench.a_operand_used(plan(16, 8, -1, 4), "default") == "dense"       # no compact copy
+    assert bench.a_operand_used(plan(32, 32, 10, 4), "default") == "dense"
+    assert bench.a_operand_used(plan(32, 32, 10, 4), "compact") == "compact"
