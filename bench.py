@@ -419,7 +419,7 @@ def main():
                      "traffic": measured_traffic(m.name, N, args.kernel, knobs
                                                  if args.schedule == "auto" and not args.tile_b
                                                  and args.row_order == "identity" and not args.mtx
-                                                 and args.blk == "16x8" else None),
+                                                 else None, args.blk),
                      "algorithmic_bytes": int(ab), "compulsory_bytes": int(compulsory),
                      "compulsory_frac": round(compulsory / t_s / 1e9 / HBM_PEAK_GBS, 4),
                      "mfma_padded_tflops": round(padded_flops / t_s / 1e12, 3),
@@ -443,15 +443,16 @@ def main():
     print(json.dumps(result), flush=True)
 
 
-def measured_traffic(workload, N, kernel, knobs):
+def measured_traffic(workload, N, kernel, knobs, blk="16x8"):
     """HBM bytes per launch of the dominant kernel from the committed
     rocprofv3 PMC summary (FETCH_SIZE and WRITE_SIZE runs, scaled by the
     copy-kernel calibration), from the profile of this workload whose
-    "knobs:" line matches the launch settings this run used; None if there
-    is none."""
+    "knobs:" line (block shape included; 16x8 when the line names none)
+    matches the launch settings this run used; None if there is none."""
     if kernel != "srbcrs" or knobs is None:
         return None
     want = {k: str(knobs[k]) for k in ("depth", "wg_cols", "grid_order", "windows_per_wave", "a_operand")}
+    want["blk"] = blk
     for path in sorted((ROOT / "profiles").glob(f"spmm_stream_{workload.replace('^', '')}_N{N}*.md")):
         traffic, prof_knobs = None, None
         for line in path.read_text().splitlines():
@@ -459,7 +460,7 @@ def measured_traffic(workload, N, kernel, knobs):
                 traffic = int(line.split(":", 1)[1])
             elif line.startswith("knobs:"):
                 prof_knobs = dict(kv.split("=") for kv in line.split(":", 1)[1].split())
-        if prof_knobs and {"windows_per_wave": "1", **prof_knobs} == want:
+        if prof_knobs and {"windows_per_wave": "1", "blk": "16x8", **prof_knobs} == want:
             return traffic
     return None
 

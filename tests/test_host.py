@@ -379,6 +379,8 @@ def test_bench_byte_model_and_traffic_lookup():
     assert isinstance(got, int) and got > 0
     assert bench.measured_traffic("uniform-65536", 512, "srbcrs", {**knobs, "depth": "3"}) is None
     assert bench.measured_traffic("uniform-65536", 512, "csr", knobs) is None
+    assert bench.measured_traffic("uniform-65536", 512, "srbcrs", knobs, "32x32") is None or \
+        knobs.get("blk") == "32x32"
 
 
 def test_bench_reports_the_library_default_a_operand():
