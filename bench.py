@@ -58,6 +58,8 @@ def parse():
                     help="SR-BCRS block shape (16x8: preprocess_gpu_16x8; 32x32: the base preprocess_gpu)")
     ap.add_argument("--no-tune", action="store_true",
                     help="skip srbcrs_plan_tune (the one-time launch-setting search run before the warm-up)")
+    ap.add_argument("--b-stage", default="default", choices=["default", "registers", "lds"],
+                    help="kernel knob: where the ring holds the gathered B rows")
     ap.add_argument("--a-operand", default="default", choices=["default", "compact", "dense"],
                     help="block-value copy the kernel reads (default: compact when blocks are at most half full)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
@@ -274,7 +276,8 @@ def gcn_train_bench(args):
 
 def tuned_knobs(t, tune_s):
     return {"depth": t["depth"], "tile_b": 0, "wg_cols": t["wg_cols"], "grid_order": t["grid_order"],
-            "windows_per_wave": t["windows_per_wave"], "a_operand": t["a_operand"], "tuned": True,
+            "windows_per_wave": t["windows_per_wave"], "a_operand": t["a_operand"], "b_stage": t["b_stage"],
+            "tuned": True,
             "tune_s": round(tune_s, 3)}
 
 
@@ -351,7 +354,7 @@ def main():
     max_col = plan.max_col
 
     explicit = bool(args.depth or args.tile_b or args.wg_cols or args.grid_order or args.wpw
-                    or args.a_operand != "default")
+                    or args.a_operand != "default" or args.b_stage != "default")
     tuned, tune_s = None, 0.0
     if args.kernel == "srbcrs" and not args.no_tune and not explicit:
         t0 = time.time()
@@ -360,7 +363,8 @@ def main():
         tune_s = time.time() - t0
     if args.kernel == "srbcrs":
         step = lambda: plan.run(B, C, depth=args.depth, tile_b=args.tile_b, wg_cols=args.wg_cols,
-                                grid_order=args.grid_order, windows_per_wave=args.wpw, a_operand=args.a_operand)
+                                grid_order=args.grid_order, windows_per_wave=args.wpw, a_operand=args.a_operand,
+                                b_stage=args.b_stage)
     else:
         step = lambda: csr_spmm(rowptr_d, colind_d, values_d, B, m.M, max_col=max_col, out=C)
 
@@ -387,7 +391,8 @@ def main():
     knobs = tuned_knobs(tuned, tune_s) if tuned else \
         {"depth": args.depth or 2, "tile_b": args.tile_b, "wg_cols": args.wg_cols or 128,
          "grid_order": args.grid_order or 1, "windows_per_wave": args.wpw or 1,
-         "a_operand": a_operand_used(plan, args.a_operand), "tuned": False}
+         "a_operand": a_operand_used(plan, args.a_operand),
+         "b_stage": "lds" if args.b_stage == "lds" else "registers", "tuned": False}
     ab = algorithmic_bytes(m.M, N, Mo, nb, m.nnz, args.kernel, bh, bw)
     compulsory = (nb * (bw * 4 + bh * bw * 4) + 4 * (Mo + 1) if args.kernel == "srbcrs" else 8 * m.nnz) \
         + m.K * N * 4 + m.M * N * 4
@@ -453,6 +458,7 @@ def measured_traffic(workload, N, kernel, knobs, blk="16x8"):
         return None
     want = {k: str(knobs[k]) for k in ("depth", "wg_cols", "grid_order", "windows_per_wave", "a_operand")}
     want["blk"] = blk
+    want["b_stage"] = str(knobs.get("b_stage", "registers"))
     for path in sorted((ROOT / "profiles").glob(f"spmm_stream_{workload.replace('^', '')}_N{N}*.md")):
         traffic, prof_knobs = None, None
         for line in path.read_text().splitlines():
@@ -460,7 +466,7 @@ def measured_traffic(workload, N, kernel, knobs, blk="16x8"):
                 traffic = int(line.split(":", 1)[1])
             elif line.startswith("knobs:"):
                 prof_knobs = dict(kv.split("=") for kv in line.split(":", 1)[1].split())
-        if prof_knobs and {"windows_per_wave": "1", "blk": "16x8", **prof_knobs} == want:
+        if prof_knobs and {"windows_per_wave": "1", "blk": "16x8", "b_stage": "registers", **prof_knobs} == want:
             return traffic
     return None
 

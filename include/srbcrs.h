@@ -223,7 +223,15 @@ int srbcrs_run(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int64_
  *                chunk-major in dispatch order, all XCDs on one chunk at a
  *                time (its B rows shared through the memory-side cache);
  *   windows_per_wave  "row" schedule: consecutive row windows one wave
- *                streams through its register ring (0 = 1), in [0, 4096].
+ *                streams through its register ring (0 = 1), in [0, 4096];
+ *   a_operand    see SRBCRS_A_* below;
+ *   b_stage      where the ring holds the gathered B rows: SRBCRS_B_DEFAULT
+ *                (= registers), SRBCRS_B_REGISTERS, or SRBCRS_B_LDS: LDS
+ *                slots filled by direct-to-LDS loads (global_load_lds) and
+ *                read back in the MFMA layout; the reference's cp.async
+ *                double buffer (kernel.inc:584-642) in gfx950 form.  LDS
+ *                staging applies at vector width 4 (tile_b 64 and 16-byte
+ *                aligned B, ldb % 4 == 0); other launches use registers.
  * Values outside these sets are rejected.  Every setting yields the same
  * bits: the per-element accumulation order does not depend on them. */
 typedef struct srbcrs_run_opts {
@@ -233,6 +241,7 @@ typedef struct srbcrs_run_opts {
   int32_t grid_order;
   int32_t windows_per_wave;
   int32_t a_operand;
+  int32_t b_stage;
 } srbcrs_run_opts;
 
 /* a_operand: where the kernel reads the block values from.  Both give the
@@ -245,6 +254,10 @@ typedef struct srbcrs_run_opts {
 #define SRBCRS_A_DEFAULT 0
 #define SRBCRS_A_COMPACT 1
 #define SRBCRS_A_DENSE 2
+
+#define SRBCRS_B_DEFAULT 0
+#define SRBCRS_B_REGISTERS 1
+#define SRBCRS_B_LDS 2
 
 #define SRBCRS_GRID_DEFAULT 0
 #define SRBCRS_GRID_CHUNK_MAJOR 1

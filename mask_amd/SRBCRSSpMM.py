@@ -113,11 +113,13 @@ class Plan:
         return self.nnz / max(1, self.total_blocks * self.blk_h * self.blk_w)
 
     def run(self, dense: Tensor, out: Optional[Tensor] = None, depth: int = 0, tile_b: int = 0, wg_cols: int = 0,
-            grid_order: int = 0, windows_per_wave: int = 0, a_operand: str = "default") -> Tensor:
+            grid_order: int = 0, windows_per_wave: int = 0, a_operand: str = "default",
+            b_stage: str = "default") -> Tensor:
         """out[:num_nodes] = A @ dense on the current stream.  The keyword
         knobs are the kernel template parameters (srbcrs_run_opts; 0 =
         default; grid_order 1 = chunk-major, 2 = window-major, 3 = chunk sweep; a_operand
-        "compact" / "dense" picks the block-value copy the kernel reads)."""
+        "compact" / "dense" picks the block-value copy the kernel reads; b_stage
+        "registers" / "lds" where the ring holds the gathered B rows)."""
         if out is None:
             out = torch.empty((self.num_nodes, dense.shape[1]), dtype=torch.float32, device=dense.device)
         if dense.dtype != torch.float32 or out.dtype != torch.float32:
@@ -127,7 +129,7 @@ class Plan:
         if out.shape[1] != dense.shape[1]:
             raise RuntimeError("out and dense must have the same number of columns")
         opts = _capi.RunOpts(int(depth), int(tile_b), int(wg_cols), int(grid_order), int(windows_per_wave),
-                             _capi.A_OPERANDS[a_operand])
+                             _capi.A_OPERANDS[a_operand], _capi.B_STAGES[b_stage])
         with torch.cuda.device(self.device):
             _capi.check(_capi.lib().srbcrs_run_ex(self._h, dense.data_ptr(), int(dense.shape[0]), int(dense.shape[1]),
                                                   int(dense.stride(0)), out.data_ptr(), int(out.stride(0)),
@@ -153,7 +155,8 @@ class Plan:
         self.tuned_widths.add(int(dense.shape[1]))
         inv = {v: k for k, v in _capi.A_OPERANDS.items()}
         return {"depth": best.depth, "wg_cols": best.wg_cols, "grid_order": best.grid_order,
-                "windows_per_wave": best.windows_per_wave or 1, "a_operand": inv[best.a_operand]}
+                "windows_per_wave": best.windows_per_wave or 1, "a_operand": inv[best.a_operand],
+                "b_stage": "lds" if best.b_stage == 2 else "registers"}
 
     def row_order(self):
         """The plan's row order (new -> original) as a numpy array."""

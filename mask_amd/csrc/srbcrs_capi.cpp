@@ -615,7 +615,8 @@ void create_on_device(srbcrs_plan& plan, const int32_t* rowptr, const int32_t* c
 }
 
 bool all_default(const srbcrs_run_opts& o) {
-  return !o.depth && !o.tile_b && !o.wg_cols && !o.grid_order && !o.windows_per_wave && !o.a_operand;
+  return !o.depth && !o.tile_b && !o.wg_cols && !o.grid_order && !o.windows_per_wave && !o.a_operand &&
+         !o.b_stage;
 }
 
 // Compact copy of the block values (srbcrs_compact.hip).  A plan too large
@@ -1036,6 +1037,9 @@ int srbcrs_run_ex(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int
       if (opts->tile_b) max_vec = opts->tile_b / 16;
       if (opts->a_operand < 0 || opts->a_operand > 2)
         fail(SRBCRS_EINVAL, "a_operand must be 0, 1 or 2 (got %d)", opts->a_operand);
+      if (opts->b_stage < 0 || opts->b_stage > 2)
+        fail(SRBCRS_EINVAL, "b_stage must be 0, 1 or 2 (got %d)", opts->b_stage);
+      ro.b_lds = opts->b_stage == SRBCRS_B_LDS;
     }
     if (!plan) fail(SRBCRS_EINVAL, "plan is NULL");
     if (opts && opts->a_operand == SRBCRS_A_COMPACT && !plan->d_awords && plan->total > 0)

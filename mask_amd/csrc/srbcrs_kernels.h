@@ -14,6 +14,7 @@ struct RunOpts {
   int chunk_major = 1;       // grid order: 0 window-major, 1 chunk-major, 2 chunk sweep (no XCD blocking)
   int windows_per_wave = 1;  // row schedule: consecutive windows streamed per wave
   int a_compact = 1;         // read A from the compact copy when the plan has one
+  int b_lds = 0;             // stage B through LDS (direct-to-LDS loads; vector width 4 only)
 };
 
 // Operands shared by every SR-BCRS launch.

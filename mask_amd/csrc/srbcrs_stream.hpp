@@ -34,10 +34,11 @@
 // VEC-wide vector load per (B row, g) per lane, VEC MFMAs per k-step, g and
 // row half.  For VEC = 4 a wave's B load covers four 256-byte row segments.
 //
-// No LDS: every B element is used by exactly one wave (waves split N), so
-// staging through LDS adds no reuse; latency is hidden by a register ring
-// DEPTH units deep, with the B-row indices fetched one ring further ahead
-// (by scalar loads, see UnitRows).
+// B ring.  Every B element is used by exactly one wave (waves split N), so
+// staging through LDS adds no reuse; by default latency is hidden by a
+// register ring DEPTH units deep, with the B-row indices fetched one ring
+// further ahead (by scalar loads, see UnitRows).  BSTAGE 1 stages the ring
+// through LDS with direct-to-LDS loads instead (LdsB).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -211,7 +212,100 @@ struct UnitRows {
     const int y0 = b0 ? lo.w : lo.y, y1 = b0 ? hi.w : hi.y;
     return int2{b1 ? x1 : x0, b1 ? y1 : y0};
   }
+  template <int I>
+  __device__ __forceinline__ int get() const {
+    static_assert(I >= 0 && I < 8, "unit row index");
+    if constexpr (I == 0) return lo.x;
+    else if constexpr (I == 1) return lo.y;
+    else if constexpr (I == 2) return lo.z;
+    else if constexpr (I == 3) return lo.w;
+    else if constexpr (I == 4) return hi.x;
+    else if constexpr (I == 5) return hi.y;
+    else if constexpr (I == 6) return hi.z;
+    else return hi.w;
+  }
 };
+
+// B staged through LDS (BSTAGE = 1).  Each wave owns DEPTH private LDS
+// slots of 8 rows x WCOLS floats; a unit's 8 B-row segments are copied
+// into its slot by direct-to-LDS loads (global_load_lds_dwordx4: each lane
+// supplies a 16-byte global address, the wave's 64 x 16 bytes land
+// contiguously at the slot offset), then read back with ds_read_b128 in
+// the MFMA lane layout.  No data is shared between waves, so no barrier is
+// needed; ordering is by the wave's own counters:
+//  - the compiler does not order LDS reads after the direct-to-LDS loads
+//    that write them, so before reading slot d the wave waits until at
+//    most (DEPTH-1)*IPU vector-memory operations are outstanding: every
+//    slot is refilled on every ring step (at the tail with the last unit
+//    again), so exactly that many direct-to-LDS loads were issued after
+//    slot d's, and vmcnt retires in order;
+//  - a slot is refilled only after lgkmcnt(0), i.e. after its reads have
+//    returned;
+//  - the wave drains vmcnt before it exits, so no load writes the LDS of a
+//    workgroup that has ended.
+template <int WCOLS>
+struct LdsB {
+  static constexpr int LPR = WCOLS / 4;    // lanes per B-row segment (16 bytes each)
+  static constexpr int RPI = 64 / LPR;     // rows per load instruction
+  static constexpr int IPU = 8 / RPI;      // load instructions per unit
+  static constexpr int SLOT = 8 * WCOLS;   // floats per slot
+  static_assert(WCOLS == 64 || WCOLS == 128, "LDS staging covers 64- and 128-column waves");
+
+  template <int M>
+  __device__ __forceinline__ static int row_of(const UnitRows& r, int sub) {
+    if constexpr (RPI == 2) {
+      return sub ? r.template get<2 * M + 1>() : r.template get<2 * M>();
+    } else {   // RPI == 4
+      const int x = (sub & 1) ? r.template get<4 * M + 1>() : r.template get<4 * M>();
+      const int y = (sub & 1) ? r.template get<4 * M + 3>() : r.template get<4 * M + 2>();
+      return (sub & 2) ? y : x;
+    }
+  }
+  template <int M>
+  __device__ __forceinline__ static void issue_one(float* slot, const float* __restrict__ B, const UnitRows& r,
+                                                   int64_t ldb, int wcol, int lane) {
+    typedef __attribute__((address_space(3))) void lds_void;
+    const int row = row_of<M>(r, lane / LPR);
+    const float* g = B + (int64_t)row * ldb + wcol + 4 * (lane % LPR);
+    __builtin_amdgcn_global_load_lds(g, (lds_void*)(slot + M * RPI * WCOLS), 16, 0, 0);
+  }
+  __device__ __forceinline__ static void issue(float* slot, const float* __restrict__ B, const UnitRows& r,
+                                               int64_t ldb, int wcol, int lane) {
+    issue_one<0>(slot, B, r, ldb, wcol, lane);
+    issue_one<1>(slot, B, r, ldb, wcol, lane);
+    if constexpr (IPU == 4) {
+      issue_one<2>(slot, B, r, ldb, wcol, lane);
+      issue_one<3>(slot, B, r, ldb, wcol, lane);
+    }
+  }
+  // lane (k, j): k-step 0 reads row 2k, k-step 1 row 2k+1, columns 4j.. of each group
+  template <int H, int G>
+  __device__ __forceinline__ static void read(Frag<H, 4, G>& f, const float* slot, int lane) {
+    const int k = lane >> 4, j = lane & 15;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      f.b0[g] = *reinterpret_cast<const f4*>(slot + (2 * k) * WCOLS + 64 * g + 4 * j);
+      f.b1[g] = *reinterpret_cast<const f4*>(slot + (2 * k + 1) * WCOLS + 64 * g + 4 * j);
+    }
+  }
+};
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their
+// maxima).  The empty asm statements with a memory clobber keep the
+// compiler from moving memory accesses across the wait.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+  asm volatile("" ::: "memory");
+}
+__device__ __forceinline__ void wait_lgkmcnt0() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+  asm volatile("" ::: "memory");
+}
 
 template <int H, int VEC, int G>
 __device__ __forceinline__ void mma_frag(const Frag<H, VEC, G>& f, f4 (&acc)[H][G][VEC]) {
@@ -330,7 +424,11 @@ __device__ __forceinline__ void flush_task(const Src& src, int t, f4 (&acc)[BH /
 // slower on the GPU (GCN N=256 1.83 -> 2.02 ms), because the tighter budget
 // delays the ring's loads.  With the compact A source (129 registers, 3
 // waves) forcing 4 waves is slower too (uniform 0.259 -> 0.274 ms).
-template <class Src, int BH, int BW, int VEC, int G, int WAVES, int DEPTH, class AF>
+//
+// BSTAGE 0 keeps the B ring in registers; BSTAGE 1 stages B through LDS
+// (LdsB, VEC = 4 only): the ring then holds only the A fragments and the
+// B-row indices in registers.  Both feed the MFMAs the same values.
+template <class Src, int BH, int BW, int VEC, int G, int WAVES, int DEPTH, class AF, int BSTAGE = 0>
 __global__ __launch_bounds__(64 * WAVES) void spmm_stream(
     Src src, const float* __restrict__ B, float* __restrict__ C, float* __restrict__ partial,
     const int* __restrict__ sidx, AF asrc, int M, int N, int64_t ldb,
@@ -376,6 +474,51 @@ __global__ __launch_bounds__(64 * WAVES) void spmm_stream(
     UnitRows idx[DEPTH];
     typename AF::template Meta<S::H> am[DEPTH];
     const int64_t last = ue - 1;
+    if constexpr (BSTAGE == 1) {
+      static_assert(VEC == 4, "LDS staging reads 16-byte B vectors");
+      typedef LdsB<WCOLS> L;
+      __shared__ __attribute__((aligned(16))) float lds_ring[WAVES * DEPTH * L::SLOT];
+      float* my_ring = lds_ring + wave * DEPTH * L::SLOT;
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+        const int64_t u = us + d < last ? us + d : last;
+        UnitRows r;
+        r.load(sidx, u);
+        asrc.template load<BH, BW>(f[d].a, u, asrc.template meta<BH, BW>(u, lane), a_off, lane);
+        L::issue(my_ring + d * L::SLOT, B, r, ldb, wcol, lane);
+        const int64_t nu = us + DEPTH + d < last ? us + DEPTH + d : last;
+        idx[d].load(sidx, nu);
+        am[d] = asrc.template meta<BH, BW>(nu, lane);
+      }
+      for (int64_t base = us; base < ue; base += DEPTH) {
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d) {
+          const int64_t u = base + d;
+          wait_vmcnt<(DEPTH - 1) * L::IPU>();
+          __builtin_amdgcn_sched_barrier(0);
+          if (u < ue) {
+            while (u >= tend) {
+              flush_task<Src, BH, VEC, G>(src, t, acc, C, partial, M, ldc, col0, lane);
+              ++t;
+              tend = src.end(t) * S::Q;
+            }
+            L::template read<S::H, G>(f[d], my_ring + d * L::SLOT, lane);
+            mma_frag<S::H, VEC, G>(f[d], acc);
+          }
+          wait_lgkmcnt0();
+          __builtin_amdgcn_sched_barrier(0);
+          // refill the slot on every step (the last unit again past the end)
+          // so the count of younger loads in the wait above stays exact
+          const int64_t nu = u + DEPTH < last ? u + DEPTH : last;
+          asrc.template load<BH, BW>(f[d].a, nu, am[d], a_off, lane);
+          L::issue(my_ring + d * L::SLOT, B, idx[d], ldb, wcol, lane);
+          const int64_t nn = u + 2 * DEPTH < last ? u + 2 * DEPTH : last;
+          idx[d].load(sidx, nn);
+          am[d] = asrc.template meta<BH, BW>(nn, lane);
+        }
+      }
+      wait_vmcnt<0>();
+    } else {
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {
       const int64_t u = us + d < last ? us + d : last;
@@ -407,6 +550,7 @@ __global__ __launch_bounds__(64 * WAVES) void spmm_stream(
           am[d] = asrc.template meta<BH, BW>(nn, lane);
         }
       }
+    }
     }
   }
   for (; t < t1; ++t) flush_task<Src, BH, VEC, G>(src, t, acc, C, partial, M, ldc, col0, lane);

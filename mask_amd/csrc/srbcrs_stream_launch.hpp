@@ -17,7 +17,7 @@ static int pick_waves(int N, int wcols, int wg_cols) {
   return w >= 4 ? 4 : (w >= 2 ? 2 : 1);
 }
 
-template <class AF, class Src, int BH, int BW, int VEC, int G, int DEPTH>
+template <class AF, class Src, int BH, int BW, int VEC, int G, int DEPTH, int BSTAGE = 0>
 static hipError_t launch_vg(const Src& src, const AF& af, int n_groups, const StreamArgs& a, const RunOpts& o,
                             hipStream_t st) {
   constexpr int WCOLS = 16 * VEC * G;
@@ -29,7 +29,7 @@ static hipError_t launch_vg(const Src& src, const AF& af, int n_groups, const St
   if (nwg > INT32_MAX) return hipErrorInvalidConfiguration;
   dim3 grid((unsigned)nwg);
 #define SRBCRS_LAUNCH(W)                                                                       \
-  hipLaunchKernelGGL((spmm_stream<Src, BH, BW, VEC, G, W, DEPTH, AF>), grid, dim3(64 * W), 0, st, \
+  hipLaunchKernelGGL((spmm_stream<Src, BH, BW, VEC, G, W, DEPTH, AF, BSTAGE>), grid, dim3(64 * W), 0, st, \
                      src, a.B, a.C, a.partial, a.sidx, af, a.M, a.N, a.ldb, a.ldc,          \
                      n_chunks, o.chunk_major)
   switch (waves) {
@@ -41,6 +41,8 @@ static hipError_t launch_vg(const Src& src, const AF& af, int n_groups, const St
   return hipGetLastError();
 }
 
+// b_lds selects the LDS-staged B ring (BSTAGE 1) at vector width 4; other
+// widths keep the register ring.
 // vec (4, 2 or 1; 16*vec divides N) is chosen by the caller from N, the
 // leading dimensions and pointer alignment.  16x8: G = 2 column groups per
 // wave when the 128-column wave tile divides N and wider-than-64 workgroups
@@ -53,12 +55,18 @@ template <class AF, class Src, int DEPTH>
 static hipError_t launch_d(const Src& src, const AF& af, int n_groups, const StreamArgs& a, int vec,
                            const RunOpts& o, hipStream_t st) {
   if (a.blk_h == 32) {
+    if (vec == 4 && o.b_lds)
+      return (a.N % 128 == 0 && o.wg_cols >= 256) ? launch_vg<AF, Src, 32, 32, 4, 2, DEPTH, 1>(src, af, n_groups, a, o, st)
+                                                 : launch_vg<AF, Src, 32, 32, 4, 1, DEPTH, 1>(src, af, n_groups, a, o, st);
     if (vec == 4)
       return (a.N % 128 == 0 && o.wg_cols >= 256) ? launch_vg<AF, Src, 32, 32, 4, 2, DEPTH>(src, af, n_groups, a, o, st)
                                                  : launch_vg<AF, Src, 32, 32, 4, 1, DEPTH>(src, af, n_groups, a, o, st);
     if (vec == 2) return launch_vg<AF, Src, 32, 32, 2, 1, DEPTH>(src, af, n_groups, a, o, st);
     return launch_vg<AF, Src, 32, 32, 1, 1, DEPTH>(src, af, n_groups, a, o, st);
   }
+  if (vec == 4 && o.b_lds)
+    return (a.N % 128 == 0 && o.wg_cols != 64) ? launch_vg<AF, Src, 16, 8, 4, 2, DEPTH, 1>(src, af, n_groups, a, o, st)
+                                              : launch_vg<AF, Src, 16, 8, 4, 1, DEPTH, 1>(src, af, n_groups, a, o, st);
   if (vec == 4)
     return (a.N % 128 == 0 && o.wg_cols != 64) ? launch_vg<AF, Src, 16, 8, 4, 2, DEPTH>(src, af, n_groups, a, o, st)
                                               : launch_vg<AF, Src, 16, 8, 4, 1, DEPTH>(src, af, n_groups, a, o, st);

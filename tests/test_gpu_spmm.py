@@ -185,9 +185,15 @@ def test_knobs_are_bitwise_invariant(gpu, blk):
     for depth, tile_b, wgc, go, wpw in itertools.product([2, 4, 8], [0, 16, 32], [0, 64, 256], [1, 2, 3], [1, 3, 16]):
         out = plan.run(dB, depth=depth, tile_b=tile_b, wg_cols=wgc, grid_order=go, windows_per_wave=wpw)
         assert np.array_equal(out.cpu().numpy(), ref), (depth, tile_b, wgc, go, wpw)
+    # B staged through LDS by direct-to-LDS loads: same MFMA inputs, same bits
+    for depth, wgc, go, wpw, a_op in itertools.product([2, 4, 8], [0, 64, 128, 256], [1, 3], [1, 3],
+                                                       ["compact", "dense"]):
+        out = plan.run(dB, depth=depth, wg_cols=wgc, grid_order=go, windows_per_wave=wpw, a_operand=a_op,
+                       b_stage="lds")
+        assert np.array_equal(out.cpu().numpy(), ref), ("lds", depth, wgc, go, wpw, a_op)
     for pol in (("split", 0), ("strict_lb", 7), ("multi_bind", 0)):
         plan.set_schedule(*pol)
         base = plan.run(dB).cpu().numpy()
-        for depth, wgc, go in itertools.product([4, 8], [0, 64, 512], [1, 2, 3]):
-            out = plan.run(dB, depth=depth, wg_cols=wgc, grid_order=go)
-            assert np.array_equal(out.cpu().numpy(), base), (pol, depth, wgc, go)
+        for depth, wgc, go, bst in itertools.product([4, 8], [0, 64, 512], [1, 2, 3], ["registers", "lds"]):
+            out = plan.run(dB, depth=depth, wg_cols=wgc, grid_order=go, b_stage=bst)
+            assert np.array_equal(out.cpu().numpy(), base), (pol, depth, wgc, go, bst)

@@ -27,12 +27,13 @@ def test_random_case(gpu, seed):
     depth = int(rng.choice([0, 2, 4, 8]))
     wg = int(rng.choice([0, 64, 128, 256]))
     order = int(rng.integers(0, 4))
+    b_stage = ["registers", "lds"][seed % 2]
     dens = float(rng.choice([0.001, 0.01, 0.05, 0.2]))
     rp, ci, vv = random_csr(M, K, dens, seed=seed, unsorted=bool(seed % 3 == 0), duplicates=bool(seed % 4 == 0),
                             empty_rows=float(rng.choice([0.0, 0.3])), heavy_rows=int(rng.integers(0, 3)),
                             heavy_len=min(K, int(rng.integers(1, 1200))))
     print("[case] sweep", seed, dict(M=M, K=K, N=N, pad_b=pad_b, pad_c=pad_c, blk=blk, policy=policy, depth=depth,
-                                     wg=wg, order=order, dens=dens, nnz=int(rp[-1])), flush=True)
+                                     wg=wg, order=order, b_stage=b_stage, dens=dens, nnz=int(rp[-1])), flush=True)
     t = lambda a: torch.from_numpy(a).cuda()
     plan = Plan(t(rp), t(ci), t(vv), M, blk[0], blk[1])
     plan.set_schedule(*policy)
@@ -43,7 +44,7 @@ def test_random_case(gpu, seed):
     for a_op in ("compact", "dense"):
         Cbig = torch.full((M + 3, N + pad_c), -3.0, device="cuda")
         C = Cbig[:, :N]
-        plan.run(Bbig[:, :N], C, depth=depth, wg_cols=wg, grid_order=order, a_operand=a_op)
+        plan.run(Bbig[:, :N], C, depth=depth, wg_cols=wg, grid_order=order, a_operand=a_op, b_stage=b_stage)
         torch.cuda.synchronize()
         cb = Cbig.cpu().numpy()
         assert (cb[:, N:] == -3.0).all() and (cb[M:, :] == -3.0).all(), "write outside C[:M, :N]"

@@ -368,7 +368,8 @@ def test_bench_byte_model_and_traffic_lookup():
         4 * (Mo + 1) + nb // 8 * (32 * 4 + 1024 * 4) + nb // 8 * 32 * N * 4 + M * N * 4
     assert bench.algorithmic_bytes(10, 64, 1, 1, 100, "csr") == 4 * 11 + 8 * 100 + 4 * 64 * 100 + 4 * 10 * 64
     from pathlib import Path
-    prof = sorted((Path(bench.ROOT) / "profiles").glob("spmm_stream_uniform-65536_N512_*.md"))
+    prof = sorted(p for p in (Path(bench.ROOT) / "profiles").glob("spmm_stream_uniform-65536_N512_*.md")
+                  if "_blk" not in p.name)
     assert prof, "no committed uniform profile"
     knobs = None
     for line in prof[0].read_text().splitlines():
