@@ -197,3 +197,20 @@ def test_knobs_are_bitwise_invariant(gpu, blk):
         for depth, wgc, go, bst in itertools.product([4, 8], [0, 64, 512], [1, 2, 3], ["registers", "lds"]):
             out = plan.run(dB, depth=depth, wg_cols=wgc, grid_order=go, b_stage=bst)
             assert np.array_equal(out.cpu().numpy(), base), (pol, depth, wgc, go, bst)
+
+
+@pytest.mark.parametrize("blk", [(16, 8), (32, 32)])
+def test_lds_stage_largest_lds_footprint(gpu, blk):
+    """LDS-staged B at its largest per-workgroup footprint (4 waves x depth 8
+    x 8 rows x 128 columns = 128 KB of the 160 KB LDS): launches and gives
+    the register ring's bits."""
+    torch = _torch()
+    M, K, N = 200, 300, 512
+    rowptr, colind, values = random_csr(M, K, 0.05, seed=77, heavy_rows=2, heavy_len=250)
+    B = np.random.default_rng(5).uniform(-1, 1, (K, N)).astype(np.float32)
+    _say("lds footprint", blk)
+    ref, plan = _run_plan(rowptr, colind, values, M, B, blk=blk)
+    dB = torch.from_numpy(B).cuda()
+    for depth in (2, 4, 8):
+        out = plan.run(dB, depth=depth, wg_cols=512, b_stage="lds")
+        assert np.array_equal(out.cpu().numpy(), ref), depth
