@@ -61,7 +61,7 @@ def build(verbose: bool = False) -> Path:
         return str(obj)
 
     with ThreadPoolExecutor(max_workers=6) as ex:
-        gen = [ex.submit(build_generated_one, bm, bk) for bm, bk in GENERATED_SHAPES]
+        gen = [ex.submit(build_generated_one, bm, bk, lds) for bm, bk, lds in GENERATED_SHAPES]
         objs = list(ex.map(compile_obj, ("srbcrs_stream_compact.hip", "srbcrs_stream_dense.hip", "srbcrs_kernels.hip",
                                          "srbcrs_capi.cpp", "srbcrs_pack.cpp", "srbcrs_convert.hip",
                                          "srbcrs_compact.hip")))
@@ -74,15 +74,19 @@ def build(verbose: bool = False) -> Path:
 
 
 GENERATED = PKG / "generated"
-GENERATED_SHAPES = ((16, 8), (32, 32))
+# (block rows, block columns, B materialized in shared memory / LDS)
+GENERATED_SHAPES = ((16, 8, False), (32, 32, False), (16, 8, True))
 
 
-def build_generated_one(bm: int, bk: int) -> str:
-    """Emit and compile the default-strategy operator of the HIP emitter for
-    one SR-BCRS block shape into mask_amd/generated/."""
+def build_generated_one(bm: int, bk: int, lds: bool = False) -> str:
+    """Emit and compile an operator of the HIP emitter for one SR-BCRS block
+    shape into mask_amd/generated/: the default strategy, or (lds) one that
+    asks for B in shared memory (materialize_b_array_ref_to_smem)."""
     from .backend_registry import sr_bcrs_spec
     from .emitter import lower_format_operator
-    return lower_format_operator(sr_bcrs_spec(bm, bk), GENERATED / f"sr_bcrs_{bm}x{bk}.so")["operator_path"]
+    strategy = {"tensor_placement": {"materialize_b_array_ref_to_smem": True}} if lds else None
+    name = f"sr_bcrs_{bm}x{bk}{'_lds' if lds else ''}.so"
+    return lower_format_operator(sr_bcrs_spec(bm, bk), GENERATED / name, strategy=strategy)["operator_path"]
 
 
 if __name__ == "__main__":

@@ -22,9 +22,14 @@ Knob mapping (strategy_agent.py:81-130 -> template parameters):
   runtime_schedule.execution_policy       -> schedule (row / strict_lb / multi_bind / auto)
   runtime_schedule.task_group_tiles       -> strict_lb workload
   runtime_schedule.runtime_max_tiles_per_segment -> split cap
-Shared-memory placement, cp.async and swizzle knobs have no counterpart:
-the gfx950 kernels keep B in registers (recorded as ignored in the
-metadata).
+  tensor_placement.materialize_b_array_ref_to_smem -> BSTAGE 1: B staged
+      through LDS by direct-to-LDS loads (vector width 4 only; measured
+      slower than the register ring on every workload, so strategies for
+      gfx950 should set it False)
+The cp.async mode, swizzle and COO placement knobs have no counterpart
+(recorded as ignored in the metadata): direct-to-LDS loads need no swizzle
+(each wave reads its own slot conflict-free) and the block indices and
+values are read through the scalar cache and registers.
 """
 from __future__ import annotations
 
@@ -51,6 +56,7 @@ class KernelParams:
     waves: int = 1           # waves per workgroup (128 columns each for 16x8/VEC 4/G 2)
     depth: int = 2           # units in flight per wave
     chunk_major: bool = True
+    b_lds: bool = False      # stage B through LDS (direct-to-LDS loads) instead of registers
     schedule: str = "auto"   # row / split / strict_lb / multi_bind / auto
     schedule_param: int = 0
 
@@ -65,8 +71,8 @@ class KernelParams:
             raise ValueError("vec must be 1/2/4, col_groups 1/2, waves 1/2/4")
         if self.depth not in (2, 4, 8):
             raise ValueError("depth must be 2, 4 or 8")
-        if self.blk_m == 32 and self.col_groups != 1:
-            raise ValueError("32x32 blocks use one column group")
+        if self.b_lds and self.vec != 4:
+            raise ValueError("LDS staging of B needs vec 4 (16-byte direct-to-LDS loads)")
         if self.schedule not in ("row", "split", "strict_lb", "multi_bind", "auto"):
             raise ValueError(f"unknown schedule {self.schedule}")
 
@@ -105,8 +111,9 @@ def params_from_strategy(strategy: Any = None, plan: Optional[BackendPlan] = Non
     if policy == "auto" and cap > 0:
         policy, param = "split", cap
     g = 2 if (bm, bk) == (16, 8) and vec == 4 else 1
+    b_lds = bool(_get(strategy, "tensor_placement", "materialize_b_array_ref_to_smem", default=False)) and vec == 4
     kp = KernelParams(blk_m=bm, blk_k=bk, vec=vec, col_groups=g, waves=1, depth=depth, chunk_major=True,
-                      schedule=policy, schedule_param=param)
+                      b_lds=b_lds, schedule=policy, schedule_param=param)
     kp.validate()
     return kp
 
@@ -144,6 +151,7 @@ _SOURCE = """// Generated by mask_amd.emitter (HIP, gfx950) for SR_BCRS operator
 namespace {{
 constexpr int kBH = {bm}, kBW = {bk}, kVEC = {vec}, kG = {g}, kWAVES = {waves}, kDEPTH = {depth};
 constexpr int kChunkMajor = {chunk_major};
+constexpr int kBSTAGE = {bstage};   // 0: B ring in registers, 1: staged through LDS
 constexpr int kWCOLS = 16 * kVEC * kG;
 constexpr int kChunkCols = kWAVES * kWCOLS;
 
@@ -161,7 +169,7 @@ int launch(const Src& src, int n_groups, const float* B, float* C, float* partia
   const long long nwg = (long long)n_groups * n_chunks;
   if (nwg == 0) return 0;
   if (nwg > 0x7fffffffLL) return -1;
-  hipLaunchKernelGGL((srbcrs::spmm_stream<Src, kBH, kBW, kVEC, kG, kWAVES, kDEPTH, srbcrs::DenseA>),
+  hipLaunchKernelGGL((srbcrs::spmm_stream<Src, kBH, kBW, kVEC, kG, kWAVES, kDEPTH, srbcrs::DenseA, kBSTAGE>),
                      dim3((unsigned)nwg), dim3(64 * kWAVES), 0, st, src, B, C, partial, sidx,
                      srbcrs::DenseA{{val}}, M, N, (int64_t)ldb,
                      (int64_t)ldc, n_chunks, kChunkMajor);
@@ -237,7 +245,8 @@ def emit_source(params: KernelParams, name: str = "sr_bcrs", specialized: Option
     return _SOURCE.format(name=name, tile_b=16 * params.vec, threads=64 * params.waves, bm=params.blk_m,
                           bk=params.blk_k, depth=params.depth, wcols=params.wave_cols, specialized=spec_lines,
                           vec=params.vec, g=params.col_groups, waves=params.waves,
-                          chunk_major=int(params.chunk_major), metadata=json.dumps(meta, sort_keys=True))
+                          chunk_major=int(params.chunk_major), bstage=int(params.b_lds),
+                          metadata=json.dumps(meta, sort_keys=True))
 
 
 class HipCodeGenerator:
@@ -269,7 +278,7 @@ class HipCodeGenerator:
             raise ValueError(f"unsupported generated synchronization scope: {sync}")
         ignored = {}
         tp = _get(attrs.get("strategy_decision"), "tensor_placement")
-        for knob in ("materialize_b_array_ref_to_smem", "enable_b_array_ref_cp_async", "b_array_ref_mode",
+        for knob in ("enable_b_array_ref_cp_async", "b_array_ref_mode",
                      "b_smem_swizzle", "coo_idx_output_mem", "coo_val_output_mem", "coo_load_mode",
                      "coo_restore_swizzle"):
             v = _get(tp, knob)

@@ -76,7 +76,7 @@ def test_select_backend_targets_and_tiles():
 
 def _strategy(**kw):
     tp = SimpleNamespace(tile_b=kw.get("tile_b", 64), b_smem_swizzle="swizzle_323",
-                         materialize_b_array_ref_to_smem=True)
+                         materialize_b_array_ref_to_smem=kw.get("b_smem", False))
     pl = SimpleNamespace(enable_async_pipeline=kw.get("pipe", True), max_wait_prior=kw.get("mwp"),
                          stage_shifts=kw.get("shifts", []))
     rs = SimpleNamespace(execution_policy=kw.get("policy", "auto"), task_group_tiles=kw.get("tgt", 64),
@@ -101,6 +101,11 @@ def test_strategy_knob_mapping():
     assert params_from_strategy({"tensor_placement": {"tile_b": 16}}, plan).vec == 1
     p32 = params_from_strategy(None, select_backend(sr_bcrs_spec(32, 32)))
     assert (p32.blk_m, p32.blk_k, p32.col_groups) == (32, 32, 1)
+    # B placement: materialize_b_array_ref_to_smem -> LDS staging, at vec 4 only
+    assert params_from_strategy(_strategy(b_smem=True), plan).b_lds
+    assert not params_from_strategy(_strategy(b_smem=True, tile_b=32), plan).b_lds
+    assert not params_from_strategy(_strategy(), plan).b_lds
+    assert params_from_strategy({"tensor_placement": {"materialize_b_array_ref_to_smem": True}}, plan).b_lds
 
 
 def test_emitted_source_structure_and_determinism():
@@ -114,7 +119,8 @@ def test_emitted_source_structure_and_determinism():
     for needle in ("#define SPARSENE_GENERATED_TILE_B 64", "#define SPARSENE_GENERATED_SUPPORTS_TASK_MAPPING 1",
                    "#define SPARSENE_GENERATED_WAVE_SIZE 64", "#define SPARSENE_GENERATED_PIPELINE_DEPTH 4",
                    "constexpr int NNZ_HINT = 7;", '#include "srbcrs_stream.hpp"',
-                   "srbcrs::spmm_stream<Src, kBH, kBW, kVEC, kG, kWAVES, kDEPTH, srbcrs::DenseA>",
+                   "srbcrs::spmm_stream<Src, kBH, kBW, kVEC, kG, kWAVES, kDEPTH, srbcrs::DenseA, kBSTAGE>",
+                   "constexpr int kBSTAGE = 0;",
                    'extern "C" int sparsene_generated_run(', 'extern "C" int sparsene_generated_run_tasks(',
                    'extern "C" int sparsene_generated_reduce('):
         assert needle in src, needle
@@ -135,17 +141,19 @@ def test_emitter_rejects_other_formats_and_bad_params():
     with pytest.raises(ValueError):
         emit_source(KernelParams(depth=3))
     with pytest.raises(ValueError):
-        emit_source(KernelParams(blk_m=32, blk_k=32, col_groups=2))
+        emit_source(KernelParams(vec=2, col_groups=1, b_lds=True))
+    emit_source(KernelParams(blk_m=32, blk_k=32, col_groups=2))   # 128-column 32x32 waves, as in the library
 
 
 def test_generated_operators_are_built():
-    """build() emitted and compiled both default operators (travel with the tree)."""
+    """build() emitted and compiled the generated operators (travel with the tree)."""
     from mask_amd.build import GENERATED, GENERATED_SHAPES
-    for bm, bk in GENERATED_SHAPES:
-        so = GENERATED / f"sr_bcrs_{bm}x{bk}.so"
+    for bm, bk, lds in GENERATED_SHAPES:
+        so = GENERATED / f"sr_bcrs_{bm}x{bk}{'_lds' if lds else ''}.so"
         assert so.exists(), so
         import ctypes
         L = ctypes.CDLL(str(so))
         L.sparsene_generated_metadata.restype = ctypes.c_char_p
         meta = json.loads(L.sparsene_generated_metadata().decode())
         assert meta["kernel_params"]["blk_m"] == bm and meta["target"] == "gfx950"
+        assert meta["kernel_params"]["b_lds"] == lds

@@ -15,18 +15,21 @@ def _say(*a):
     print("[case]", *a, flush=True)
 
 
-@pytest.mark.parametrize("blk", [(16, 8), (32, 32)])
-def test_generated_operator_matches_library(gpu, blk):
+@pytest.mark.parametrize("blk,lds", [((16, 8), False), ((32, 32), False), ((16, 8), True)])
+def test_generated_operator_matches_library(gpu, blk, lds):
+    """lds: the operator of a strategy that materializes B in shared memory
+    (B staged through LDS by direct-to-LDS loads)."""
     import torch
     from mask_amd.build import GENERATED
     from mask_amd.emitter import GeneratedOperator
     from mask_amd.SRBCRSSpMM import Plan
     bh, bw = blk
-    op = GeneratedOperator(GENERATED / f"sr_bcrs_{bh}x{bw}.so")
+    op = GeneratedOperator(GENERATED / f"sr_bcrs_{bh}x{bw}{'_lds' if lds else ''}.so")
+    assert op.params.b_lds == lds
     M, K, N = 500, 3000, 256
     rowptr, colind, values = random_csr(M, K, 0.01, seed=13, heavy_rows=4, heavy_len=1200, empty_rows=0.2)
     B = np.random.default_rng(13).uniform(-1, 1, (K, N)).astype(np.float32)
-    _say("generated", blk, M, K, N)
+    _say("generated", blk, lds, M, K, N)
     plan = Plan(*(torch.from_numpy(a).cuda() for a in (rowptr, colind, values)), M, bh, bw)
     dB = torch.from_numpy(B).cuda()
     for pol, param in (("row", 0), ("split", 3), ("strict_lb", 16), ("multi_bind", 0)):
