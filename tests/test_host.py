@@ -369,7 +369,7 @@ def test_bench_byte_model_and_traffic_lookup():
     assert bench.algorithmic_bytes(10, 64, 1, 1, 100, "csr") == 4 * 11 + 8 * 100 + 4 * 64 * 100 + 4 * 10 * 64
     from pathlib import Path
     prof = sorted(p for p in (Path(bench.ROOT) / "profiles").glob("spmm_stream_uniform-65536_N512_*.md")
-                  if "_blk" not in p.name)
+                  if "_blk" not in p.name and "traffic_bytes:" in p.read_text())
     assert prof, "no committed uniform profile"
     knobs = None
     for line in prof[0].read_text().splitlines():
