@@ -38,7 +38,7 @@ def parse():
     ap.add_argument("--shard-sim", type=int, default=0,
                     help="time one GPU's share of a G-way row sharding and column sharding (one GPU, no communication)")
     ap.add_argument("--gcn-train", action="store_true",
-                    help="GCN training step (ReplaceableGCN 512-256-64 + Adam) through the srbcrs_spmm drop-in")
+                    help="GCN training step (GCN 512-256-64 + Adam) through the srbcrs_spmm drop-in")
     ap.add_argument("--gcn-forward", action="store_true",
                     help="time the GCN workload's two-layer forward instead of one SpMM")
     ap.add_argument("--row-order", default="identity",
@@ -214,20 +214,20 @@ def shard_sim_bench(args):
 
 def gcn_train_bench(args):
     """Full-batch GCN training steps on the GCN workload through the drop-in
-    path the reference's GCN script uses (eva_gcn_sparsene.py:267-343):
-    ReplaceableGCN(512, 256, 64, 2 layers, dropout 0.5) with the
+    path the reference's GCN script uses (eva_gcn_sparsene.py:267-343): a
+    two-layer GCN 512-256-64 (dropout 0.5) whose aggregations run through the
     srbcrs_spmm external backend (forward A @ X, backward A^T @ dY on the
     transposed CSR), log-softmax + NLL on synthetic labels, Adam.  Timed per
-    SR-BCRS variant (16x8 and the 32x32 base) and, for comparison, with the
-    torch backend (torch.sparse.mm on ROCm).  One JSON line."""
+    SR-BCRS variant (16x8 and the 32x32 base) and, for comparison, with
+    torch.sparse.mm on ROCm.  One JSON line."""
     import torch
     import torch.nn.functional as F
     from mask_amd import datasets
     from mask_amd.external_backend_spmm import reset_backend_state, srbcrs_spmm
-    from mask_amd.gcn import ReplaceableGCN, SpMMBackend, graph_from_csr
+    from mask_amd.gcn import GCN, graph_from_csr, torch_spmm
     dev = torch.device("cuda", 0)
     m = datasets.make_config("gcn-232965")
-    data = graph_from_csr(m, 512, dev, seed=m.seed)
+    graph = graph_from_csr(m, 512, dev, seed=m.seed)
     labels = torch.randint(0, 64, (m.M,), generator=torch.Generator().manual_seed(m.seed)).to(dev)
     if not args.no_tune:
         os.environ["SPARSENE_SRBCRS_AUTOTUNE"] = "1"   # tuned on each plan's first call per width
@@ -235,14 +235,14 @@ def gcn_train_bench(args):
     for name in ("16x8", "base", "torch"):
         os.environ["SPARSENE_SRBCRS_VARIANT"] = "16x8" if name == "torch" else name
         reset_backend_state()
-        backend = SpMMBackend("torch") if name == "torch" else SpMMBackend("external:srbcrs_spmm", srbcrs_spmm)
         torch.manual_seed(m.seed)
-        model = ReplaceableGCN(512, 256, 64, 2, 0.5).to(dev)
+        model = GCN((512, 256, 64), dropout=0.5, spmm=torch_spmm if name == "torch" else srbcrs_spmm,
+                    seed=m.seed).to(dev)
         opt = torch.optim.Adam(model.parameters(), lr=0.01)
 
         def step():
             opt.zero_grad(set_to_none=True)
-            loss = F.nll_loss(model(data, backend), labels)
+            loss = F.nll_loss(model(graph), labels)
             loss.backward()
             opt.step()
             return loss
@@ -264,7 +264,7 @@ def gcn_train_bench(args):
                          "first_step_s": round(setup_s, 3)}
         losses[name] = round(float(loss), 5)
     print(json.dumps({
-        "metric": "GCN training step time (gcn-232965, ReplaceableGCN 512-256-64, Adam, full batch)",
+        "metric": "GCN training step time (gcn-232965, GCN 512-256-64, Adam, full batch)",
         "value": results["16x8"]["ms_per_step"], "unit": "ms", "higher_is_better": False, "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "dtype": "f32",
         "data": "synthetic R-MAT graph, N(0,1) features, uniform labels (seeded)",

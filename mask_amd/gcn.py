@@ -1,18 +1,24 @@
-"""GCN with a replaceable SpMM, the caller of the SR-BCRS path.
+"""A small GCN whose neighbourhood aggregation is a pluggable CSR SpMM.
 
-Mirrors end2end/gcn/eva_gcn_sparsene.py: ``SpMMBackend`` (:189-265),
-``ReplaceableSpMMFunction`` (:267-289: forward A @ X, backward A^T @ dY
-through the same SpMM), ``ReplaceableGCNConv`` (:292-314: X @ W then the
-SpMM) and ``ReplaceableGCN`` (:317-343).  ``GraphData`` here is built from
-the seeded synthetic graphs of ``mask_amd.datasets`` (no dataset files), and
-``gcn2_forward`` is the two-layer forward relu(A (X W1)) -> A (H W2).
+This is the caller the SR-BCRS path is measured under: the reference's GCN
+script (end2end/gcn/eva_gcn_sparsene.py) trains a graph convolution network
+whose aggregation ``A @ H`` goes through an external SpMM function with the
+signature ``fn(rowptr, colind, values, dense, num_rows, feat_dim,
+num_nodes_ori)``, e.g. ``mask_amd.external_backend_spmm.srbcrs_spmm``.
+
+Design here:
+- ``Graph`` holds A and its transpose as device CSR plus node features; the
+  graphs come from the seeded synthetic matrices of ``mask_amd.datasets``.
+- ``aggregate(graph, h, fn)`` is an autograd op: forward ``A @ h`` and, since
+  d(A h)/dh applied to g is ``A^T g``, backward runs the same SpMM on the
+  transposed CSR.
+- ``GCN`` is a stack of layers ``h <- aggregate(h @ W_i)`` with ReLU and
+  dropout between layers and log-softmax at the end.
 """
 from __future__ import annotations
 
-import importlib
-import weakref
 from dataclasses import dataclass
-from typing import Callable, Dict, Optional, Tuple, cast
+from typing import Callable, Optional, Sequence, Tuple
 
 import numpy as np
 import torch
@@ -20,20 +26,8 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 Tensor = torch.Tensor
-
-
-@dataclass
-class GraphData:
-    name: str
-    num_nodes: int
-    num_edges: int
-    rowptr: Tensor
-    colind: Tensor
-    values: Tensor
-    rowptr_t: Tensor
-    colind_t: Tensor
-    values_t: Tensor
-    x: Tensor
+SpMMFn = Callable[..., Tensor]
+CSR = Tuple[Tensor, Tensor, Tensor]
 
 
 def csr_transpose(rowptr: np.ndarray, colind: np.ndarray, values: np.ndarray, n_cols: int):
@@ -46,126 +40,104 @@ def csr_transpose(rowptr: np.ndarray, colind: np.ndarray, values: np.ndarray, n_
     return t_rowptr.astype(np.int32), rows[order].astype(np.int32), values[order]
 
 
-def graph_from_csr(m, feature_dim: int, device: torch.device, seed: int = 0) -> GraphData:
-    """GraphData for a ``datasets.CSRMatrix`` with N(0,1) features."""
-    rp_t, ci_t, v_t = csr_transpose(m.rowptr, m.colind, m.values, m.K)
+@dataclass
+class Graph:
+    name: str
+    num_nodes: int
+    num_edges: int
+    a: CSR          # (rowptr, colind, values) of A on the device
+    at: CSR         # the same for A^T
+    x: Tensor       # node features, num_nodes x F
+
+
+def graph_from_csr(m, feature_dim: int, device: torch.device, seed: int = 0) -> Graph:
+    """A ``Graph`` for a ``datasets.CSRMatrix`` with N(0,1) features."""
     gen = torch.Generator(device="cpu")
     gen.manual_seed(seed)
     x = torch.randn((m.M, feature_dim), generator=gen, dtype=torch.float32)
-    to = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)
-    return GraphData(m.name, m.M, m.nnz, to(m.rowptr), to(m.colind), to(m.values), to(rp_t), to(ci_t), to(v_t),
-                     x.to(device))
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(device)
+    a = (dev(m.rowptr), dev(m.colind), dev(m.values))
+    at = tuple(dev(v) for v in csr_transpose(m.rowptr, m.colind, m.values, m.K))
+    return Graph(m.name, m.M, m.nnz, a, at, x.to(device))
 
 
-class SpMMBackend:
-    """Replaceable SpMM: ``torch`` (torch.sparse.mm) or an external function
-    with the signature fn(rowptr, colind, values, dense, num_rows, feat_dim,
-    num_nodes_ori), e.g. ``mask_amd.external_backend_spmm.srbcrs_spmm``."""
-
-    def __init__(self, name: str, external_fn: Optional[Callable[..., Tensor]] = None) -> None:
-        self.name = name
-        self.external_fn = external_fn
-        self._i32_cache: Dict[int, Tuple[weakref.ReferenceType, Tensor]] = {}
-
-    def _to_i32_cached(self, t: Tensor) -> Tensor:
-        if t.dtype == torch.int32 and t.is_contiguous():
-            return t
-        ent = self._i32_cache.get(id(t))
-        if ent is not None and ent[0]() is t:
-            return ent[1]
-        c = t.to(torch.int32).contiguous()
-        self._i32_cache[id(t)] = (weakref.ref(t), c)
-        return c
-
-    @staticmethod
-    def build(backend: str, module_name: str = "", function_name: str = "") -> "SpMMBackend":
-        if backend == "torch":
-            return SpMMBackend("torch")
-        if backend != "external":
-            raise ValueError(f"Unsupported backend: {backend}")
-        if not module_name or not function_name:
-            raise ValueError("External backend requires --external-module and --external-function")
-        fn = getattr(importlib.import_module(module_name), function_name)
-        return SpMMBackend(f"external:{module_name}.{function_name}", fn)
-
-    def spmm(self, rowptr: Tensor, colind: Tensor, values: Tensor, dense: Tensor) -> Tensor:
-        n_rows = int(rowptr.numel() - 1)
-        if self.external_fn is None:
-            csr = torch.sparse_csr_tensor(rowptr, colind, values, size=(n_rows, int(dense.shape[0])),
-                                          device=dense.device)
-            return torch.sparse.mm(csr, dense)
-        out = self.external_fn(self._to_i32_cached(rowptr), self._to_i32_cached(colind), values, dense, n_rows,
-                               int(dense.shape[1]), n_rows)
-        if isinstance(out, (tuple, list)):
-            out = out[0]
-        if not isinstance(out, torch.Tensor):
-            raise TypeError("External SpMM backend must return a torch.Tensor")
-        return out
+def torch_spmm(rowptr: Tensor, colind: Tensor, values: Tensor, dense: Tensor, num_rows: int, feat_dim: int,
+               num_nodes_ori: int) -> Tensor:
+    """The torch aggregation (torch.sparse.mm on a CSR tensor), same signature
+    as the external SpMM functions, for comparison runs."""
+    a = torch.sparse_csr_tensor(rowptr, colind, values, size=(num_rows, int(dense.shape[0])), device=dense.device)
+    return torch.sparse.mm(a, dense)
 
 
-class ReplaceableSpMMFunction(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, rowptr, colind, values, rowptr_t, colind_t, values_t, dense, backend: SpMMBackend):
-        ctx.backend = backend
-        ctx.save_for_backward(rowptr_t, colind_t, values_t)
-        return backend.spmm(rowptr, colind, values, dense.contiguous())
+def _spmm(fn: SpMMFn, csr: CSR, dense: Tensor) -> Tensor:
+    rows = int(csr[0].numel()) - 1
+    out = fn(csr[0], csr[1], csr[2], dense.contiguous(), rows, int(dense.shape[1]), rows)
+    out = out[0] if isinstance(out, (list, tuple)) else out
+    if not isinstance(out, Tensor):
+        raise TypeError("an SpMM function must return a torch.Tensor")
+    return out
+
+
+class _Aggregate(torch.autograd.Function):
+    """y = A h; dL/dh = A^T dL/dy (both through the same SpMM function)."""
 
     @staticmethod
-    def backward(ctx, *grad_outputs):
-        rowptr_t, colind_t, values_t = ctx.saved_tensors
-        grad_dense = ctx.backend.spmm(rowptr_t, colind_t, values_t, grad_outputs[0].contiguous())
-        return None, None, None, None, None, None, grad_dense, None
+    def forward(ctx, h: Tensor, graph: Graph, fn: SpMMFn) -> Tensor:
+        ctx.graph, ctx.fn = graph, fn
+        return _spmm(fn, graph.a, h)
+
+    @staticmethod
+    def backward(ctx, grad: Tensor):
+        return _spmm(ctx.fn, ctx.graph.at, grad), None, None
 
 
-class ReplaceableGCNConv(nn.Module):
-    def __init__(self, in_dim: int, out_dim: int) -> None:
-        super().__init__()
-        self.weight = nn.Parameter(torch.empty((in_dim, out_dim), dtype=torch.float32))
-        self.reset_parameters()
-
-    def reset_parameters(self) -> None:
-        nn.init.xavier_uniform_(self.weight)
-
-    def forward(self, x: Tensor, data: GraphData, backend: SpMMBackend) -> Tensor:
-        x = x @ self.weight
-        out = ReplaceableSpMMFunction.apply(data.rowptr, data.colind, data.values, data.rowptr_t, data.colind_t,
-                                            data.values_t, x, backend)
-        return cast(Tensor, out)
+def aggregate(graph: Graph, h: Tensor, fn: SpMMFn) -> Tensor:
+    """A @ h with gradients, through ``fn``."""
+    return _Aggregate.apply(h, graph, fn)
 
 
-class ReplaceableGCN(nn.Module):
-    def __init__(self, in_dim: int, hidden_dim: int, out_dim: int, num_layers: int, dropout: float) -> None:
-        super().__init__()
-        if num_layers < 2:
-            raise ValueError("num_layers must be >= 2")
-        self.conv_in = ReplaceableGCNConv(in_dim, hidden_dim)
-        self.hidden = nn.ModuleList([ReplaceableGCNConv(hidden_dim, hidden_dim) for _ in range(num_layers - 2)])
-        self.conv_out = ReplaceableGCNConv(hidden_dim, out_dim)
-        self.dropout = float(dropout)
-
-    def forward(self, data: GraphData, backend: SpMMBackend) -> Tensor:
-        x = F.relu(self.conv_in(data.x, data, backend))
-        x = F.dropout(x, p=self.dropout, training=self.training)
-        for conv in self.hidden:
-            x = F.relu(conv(x, data, backend))
-            x = F.dropout(x, p=self.dropout, training=self.training)
-        x = self.conv_out(x, data, backend)
-        return F.log_softmax(x, dim=1)
-
-
-def glorot_weights(dims, seed: int = 0, device: Optional[torch.device] = None):
-    """Glorot-uniform weights W_i of shape dims[i] x dims[i+1]."""
+def glorot_weights(dims: Sequence[int], seed: int = 0, device: Optional[torch.device] = None):
+    """Glorot-uniform weights W_i of shape dims[i] x dims[i+1]: U(-r, r) with
+    r = sqrt(6 / (fan_in + fan_out))."""
     gen = torch.Generator(device="cpu")
     gen.manual_seed(seed)
-    ws = []
-    for a, b in zip(dims[:-1], dims[1:]):
-        bound = float(np.sqrt(6.0 / (a + b)))
-        ws.append(((torch.rand((a, b), generator=gen) * 2 - 1) * bound).to(device))
-    return ws
+    out = []
+    for fan_in, fan_out in zip(dims[:-1], dims[1:]):
+        r = float(np.sqrt(6.0 / (fan_in + fan_out)))
+        out.append(((torch.rand((fan_in, fan_out), generator=gen) * 2 - 1) * r).to(device))
+    return out
 
 
-def gcn2_forward(data: GraphData, w1: Tensor, w2: Tensor, backend: SpMMBackend) -> Tensor:
-    """relu(A (X W1)) then A (H W2): the two SpMMs at N = w1.shape[1] and
-    w2.shape[1] plus the dense GEMMs."""
-    h = F.relu(backend.spmm(data.rowptr, data.colind, data.values, (data.x @ w1).contiguous()))
-    return backend.spmm(data.rowptr, data.colind, data.values, (h @ w2).contiguous())
+class GCN(nn.Module):
+    """Layers dims[0] -> dims[1] -> ... -> dims[-1]; each is
+    ``aggregate(h @ W)``, ReLU + dropout between layers, log-softmax last."""
+
+    def __init__(self, dims: Sequence[int], dropout: float = 0.0, spmm: Optional[SpMMFn] = None,
+                 seed: Optional[int] = None) -> None:
+        super().__init__()
+        if len(dims) < 3:
+            raise ValueError("a GCN needs at least two layers (three dims)")
+        if spmm is None:
+            from .external_backend_spmm import srbcrs_spmm
+            spmm = srbcrs_spmm
+        if seed is None:
+            seed = int(torch.randint(0, 2 ** 31 - 1, (1,)).item())
+        self.weights = nn.ParameterList(nn.Parameter(w) for w in glorot_weights(dims, seed))
+        self.dropout = float(dropout)
+        self.spmm = spmm
+
+    def forward(self, graph: Graph, features: Optional[Tensor] = None) -> Tensor:
+        h = graph.x if features is None else features
+        last = len(self.weights) - 1
+        for i, w in enumerate(self.weights):
+            h = aggregate(graph, h @ w, self.spmm)
+            if i < last:
+                h = F.dropout(torch.relu(h), self.dropout, self.training)
+        return torch.log_softmax(h, dim=1)
+
+
+def gcn2_forward(graph: Graph, w1: Tensor, w2: Tensor, spmm: SpMMFn) -> Tensor:
+    """relu(A (X W1)) then A (H W2): the GCN workload's two SpMMs at
+    N = w1.shape[1] and w2.shape[1] plus the dense GEMMs (no autograd)."""
+    h = torch.relu(_spmm(spmm, graph.a, graph.x @ w1))
+    return _spmm(spmm, graph.a, h @ w2)

@@ -44,22 +44,20 @@ def _dense_graph(m):
 
 
 def test_gcn_forward_backward_matches_fp64(gpu, monkeypatch):
-    """ReplaceableGCN with the SR-BCRS SpMM: loss and weight gradients match
+    """A three-layer GCN with the SR-BCRS SpMM: loss and weight gradients match
     a dense fp64 autograd reference (backward runs A^T through the SpMM)."""
     import torch
     from mask_amd import datasets, external_backend_spmm as E
-    from mask_amd.gcn import ReplaceableGCN, SpMMBackend, graph_from_csr
+    from mask_amd.gcn import GCN, graph_from_csr
     monkeypatch.setenv("SPARSENE_SRBCRS_VARIANT", "16x8")
     E.reset_backend_state()
     m = datasets.gcn_graph(n=3000, avg_degree=12, N=64)
     _say("gcn autograd", m.M, m.nnz)
     dev = torch.device("cuda", 0)
     data = graph_from_csr(m, 48, dev, seed=3)
-    torch.manual_seed(0)
-    model = ReplaceableGCN(48, 64, 16, num_layers=3, dropout=0.0).to(dev)
-    backend = SpMMBackend("external:srbcrs", E.srbcrs_spmm)
+    model = GCN((48, 64, 64, 16), dropout=0.0, spmm=E.srbcrs_spmm, seed=0).to(dev)
     y = torch.randint(0, 16, (m.M,), device=dev)
-    loss = F_nll(model(data, backend), y)
+    loss = F_nll(model(data), y)
     loss.backward()
     grads = [p.grad.double().cpu() for p in model.parameters()]
 
@@ -91,7 +89,7 @@ def test_gcn2_forward_workload(gpu, monkeypatch):
     scaled graph: each SpMM within the gate against the fp64 oracle."""
     import torch
     from mask_amd import datasets, external_backend_spmm as E
-    from mask_amd.gcn import SpMMBackend, gcn2_forward, glorot_weights, graph_from_csr
+    from mask_amd.gcn import gcn2_forward, glorot_weights, graph_from_csr
     monkeypatch.setenv("SPARSENE_SRBCRS_VARIANT", "16x8")
     E.reset_backend_state()
     m = datasets.make_config("gcn-232965", scale_down=16)
@@ -99,16 +97,14 @@ def test_gcn2_forward_workload(gpu, monkeypatch):
     dev = torch.device("cuda", 0)
     data = graph_from_csr(m, 512, dev, seed=1)
     w1, w2 = glorot_weights([512, 256, 64], seed=2, device=dev)
-    backend = SpMMBackend("external:srbcrs", E.srbcrs_spmm)
-    out = gcn2_forward(data, w1, w2, backend)
+    spmm = lambda d: E.srbcrs_spmm(*data.a, d.contiguous(), m.M, d.shape[1], m.M)
+    out = gcn2_forward(data, w1, w2, E.srbcrs_spmm)
     torch.cuda.synchronize()
     # layer by layer against the oracle on the same fp32 dense inputs
     xw = (data.x @ w1).cpu().numpy()
     h_ref, habs = oracle.csr_spmm_f64(m.rowptr, m.colind, m.values, xw, m.M, with_abs=True)
-    h = torch.relu(backend.spmm(data.rowptr, data.colind, data.values, (data.x @ w1).contiguous()))
-    met = oracle.error_metrics(torch.relu(backend.spmm(data.rowptr, data.colind, data.values,
-                                                       (data.x @ w1).contiguous())).cpu().numpy(),
-                               np.maximum(h_ref, 0), habs)
+    h = torch.relu(spmm(data.x @ w1))
+    met = oracle.error_metrics(h.cpu().numpy(), np.maximum(h_ref, 0), habs)
     assert met["max_ratio"] <= 1e-4 and met["ref_gate"], met
     hw = (h @ w2).cpu().numpy()
     o_ref, oabs = oracle.csr_spmm_f64(m.rowptr, m.colind, m.values, hw, m.M, with_abs=True)

@@ -238,13 +238,16 @@ def test_select_tile_b_and_padding(monkeypatch):
 
 def test_variant_normalisation():
     from mask_amd import external_backend_spmm as E
-    n = E.SRBCRSBackend._normalize_variant
-    assert n("") == "base" and n("SR_BCRS") == "base"
-    assert n("sr_bcrs_16x8") == "16x8"
-    assert n("multibind_16x8") == "16x8_multi_binding"
-    assert n("strict-lb") == "strict_lb"
-    assert E._VARIANT_PLAN["16x8_strict_lb"] == ((16, 8), ("strict_lb", 0))
-    assert E.SRBCRSBackend._variant_tile_shape("base") == (32, 32)
+    n = E.canonical_variant
+    assert n("") == "base" and n("SR_BCRS") == "base" and n("default") == "base"
+    assert n("sr_bcrs_16x8") == "16x8" and n("16_8") == "16x8"
+    assert n("multibind_16x8") == "16x8_multi_binding" and n("16x8_multi_bind") == "16x8_multi_binding"
+    assert n("srbcrs_16x8_strict_lb") == "16x8_strict_lb" and n("strictlb_16x8") == "16x8_strict_lb"
+    assert n("strict-lb") == "strict_lb" and n("multi-binding") == "multi_binding"
+    assert n("nonsense") == "nonsense"
+    assert E.VARIANTS["16x8_strict_lb"] == ((16, 8), ("strict_lb", 0))
+    assert E.SRBCRSBackend("base").spec.block == (32, 32)
+    assert E.SRBCRSBackend("nonsense").spec == E.VARIANTS["base"]
 
 
 def test_csr_transpose_matches_dense():
@@ -399,3 +402,35 @@ def test_bench_reports_the_library_default_a_operand():
     assert bench.a_operand_used(plan(16, 8, -1, 4), "default") == "dense"       # no compact copy
     assert bench.a_operand_used(plan(32, 32, 10, 4), "default") == "dense"
     assert bench.a_operand_used(plan(32, 32, 10, 4), "compact") == "compact"
+
+
+def test_gcn_autograd_on_cpu_with_torch_spmm():
+    """The GCN module's aggregation op on the CPU (torch.sparse.mm as the SpMM):
+    loss and gradients equal a dense fp64 autograd model with the same weights,
+    so the backward really runs A^T (a non-symmetric A catches a missing transpose)."""
+    torch = pytest.importorskip("torch")
+    from mask_amd import datasets
+    from mask_amd.gcn import GCN, graph_from_csr, torch_spmm
+    rowptr, colind, values = random_csr(60, 60, 0.08, seed=5)
+    m = datasets.CSRMatrix("tiny", rowptr, colind, values, 60, 60, 8, "uniform", 0)
+    g = graph_from_csr(m, 12, torch.device("cpu"), seed=1)
+    model = GCN((12, 10, 5), spmm=torch_spmm, seed=3)
+    y = torch.arange(60) % 5
+    loss = torch.nn.functional.nll_loss(model(g), y)
+    loss.backward()
+    A = torch.zeros(60, 60, dtype=torch.float64)
+    for r in range(60):
+        for e in range(rowptr[r], rowptr[r + 1]):
+            A[r, colind[e]] += float(values[e])
+    assert not torch.equal(A, A.T)
+    ws = [p.detach().double().clone().requires_grad_(True) for p in model.parameters()]
+    h = g.x.double()
+    for i, w in enumerate(ws):
+        h = A @ (h @ w)
+        if i < len(ws) - 1:
+            h = torch.relu(h)
+    ref = torch.nn.functional.nll_loss(torch.log_softmax(h, 1), y)
+    ref.backward()
+    assert abs(loss.item() - ref.item()) < 1e-5
+    for p, w in zip(model.parameters(), ws):
+        assert torch.allclose(p.grad.double(), w.grad, atol=1e-5, rtol=1e-4)
