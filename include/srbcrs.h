@@ -82,6 +82,8 @@ typedef struct srbcrs_plan_desc {
   int32_t packing;        /* SRBCRS_PACK_* */
   int32_t dup_policy;     /* SRBCRS_DUP_* */
   int64_t stored_values;  /* values in the compact copy of val (-1: no copy) */
+  const void *d_a_words;  /* compact copy: one {mask, base} uint32 pair per 32 block positions (NULL: none) */
+  const float *d_a_packed; /* compact copy: the stored values in logical order */
 } srbcrs_plan_desc;
 int srbcrs_plan_get(const srbcrs_plan *plan, srbcrs_plan_desc *out);
 
@@ -200,7 +202,12 @@ int srbcrs_plan_set_schedule(srbcrs_plan *plan, const char *policy, int32_t para
  * Requirements: N % 16 == 0, K > max column, c_rows >=
  * num_nodes (rows beyond num_nodes are not written).  Every row
  * < num_nodes of C is overwritten (zeros for empty windows).  Schedules
- * other than "row" use a plan-owned partial buffer grown on demand. */
+ * other than "row" use a plan-owned partial buffer, grown (hipMalloc) when a
+ * run needs more slots x ldc than it holds.  Growth never frees: replaced
+ * buffers and replaced task tables stay allocated until
+ * srbcrs_plan_destroy, so a HIP graph captured on an earlier run keeps
+ * valid addresses.  Capture after one eager run with the same N, ldc and
+ * schedule (a growing run allocates, which graph capture forbids). */
 int srbcrs_run(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int64_t ldb,
                float *d_C, int64_t ldc, int64_t c_rows, void *stream);
 

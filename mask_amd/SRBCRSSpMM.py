@@ -34,6 +34,22 @@ def _check_input(t: Tensor, name: str) -> None:
         raise RuntimeError(f"{name} must be contiguous")
 
 
+def check_operand(t: Tensor, name: str, device: torch.device) -> None:
+    """A dense operand the kernels read or write through a raw pointer: a
+    float32 tensor on ``device`` (a host tensor's address would reach the
+    GPU), 2-D, row-major (unit column stride; any row stride >= width)."""
+    if not isinstance(t, Tensor):
+        raise RuntimeError(f"{name} must be a torch tensor")
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a CUDA tensor")
+    if t.device != torch.device(device):
+        raise RuntimeError(f"{name} is on {t.device}, the plan on {device}")
+    if t.dtype != torch.float32:
+        raise RuntimeError(f"{name} must be float32")
+    if t.dim() != 2 or (t.shape[1] > 1 and t.stride(1) != 1) or t.stride(0) < max(1, t.shape[1]):
+        raise RuntimeError(f"{name} must be row-major 2-D")
+
+
 def _stream_handle(device: torch.device) -> int:
     return torch.cuda.current_stream(device).cuda_stream
 
@@ -112,6 +128,20 @@ class Plan:
         """nnz / (blocks * blk_h * blk_w): the stored-value density."""
         return self.nnz / max(1, self.total_blocks * self.blk_h * self.blk_w)
 
+    def _operands(self, dense: Tensor, out: Optional[Tensor]) -> Tensor:
+        """Validate dense (and out, allocated when None) before any launch:
+        float32 GPU tensors on the plan's device, 2-D with unit column
+        stride, the same width, and out with at least num_nodes rows."""
+        check_operand(dense, "dense", self.device)
+        if out is None:
+            out = torch.empty((self.num_nodes, dense.shape[1]), dtype=torch.float32, device=dense.device)
+        check_operand(out, "out", self.device)
+        if out.shape[1] != dense.shape[1]:
+            raise RuntimeError("out and dense must have the same number of columns")
+        if out.shape[0] < self.num_nodes:
+            raise RuntimeError(f"out has {out.shape[0]} rows, the plan writes {self.num_nodes}")
+        return out
+
     def run(self, dense: Tensor, out: Optional[Tensor] = None, depth: int = 0, tile_b: int = 0, wg_cols: int = 0,
             grid_order: int = 0, windows_per_wave: int = 0, a_operand: str = "default",
             b_stage: str = "default") -> Tensor:
@@ -120,14 +150,7 @@ class Plan:
         default; grid_order 1 = chunk-major, 2 = window-major, 3 = chunk sweep; a_operand
         "compact" / "dense" picks the block-value copy the kernel reads; b_stage
         "registers" / "lds" where the ring holds the gathered B rows)."""
-        if out is None:
-            out = torch.empty((self.num_nodes, dense.shape[1]), dtype=torch.float32, device=dense.device)
-        if dense.dtype != torch.float32 or out.dtype != torch.float32:
-            raise RuntimeError("dense and out must be float32")
-        if dense.dim() != 2 or dense.stride(1) != 1 or out.dim() != 2 or out.stride(1) != 1:
-            raise RuntimeError("dense and out must be row-major 2-D")
-        if out.shape[1] != dense.shape[1]:
-            raise RuntimeError("out and dense must have the same number of columns")
+        out = self._operands(dense, out)
         opts = _capi.RunOpts(int(depth), int(tile_b), int(wg_cols), int(grid_order), int(windows_per_wave),
                              _capi.A_OPERANDS[a_operand], _capi.B_STAGES[b_stage])
         with torch.cuda.device(self.device):
@@ -141,11 +164,7 @@ class Plan:
         srbcrs_plan_tune) and keep the fastest for later default-knob runs
         at that width; returns the choice.  out (or a scratch tensor) is
         overwritten with A @ dense."""
-        if out is None:
-            out = torch.empty((self.num_nodes, dense.shape[1]), dtype=torch.float32, device=dense.device)
-        if dense.dtype != torch.float32 or out.dtype != torch.float32 or dense.dim() != 2 or out.dim() != 2 \
-                or dense.stride(1) != 1 or out.stride(1) != 1 or out.shape[1] != dense.shape[1]:
-            raise RuntimeError("dense and out must be row-major 2-D float32 with the same number of columns")
+        out = self._operands(dense, out)
         best = _capi.RunOpts()
         with torch.cuda.device(self.device):
             _capi.check(_capi.lib().srbcrs_plan_tune(self._h, dense.data_ptr(), int(dense.shape[0]),

@@ -57,6 +57,8 @@ class PlanDesc(ctypes.Structure):
         ("packing", ctypes.c_int32),
         ("dup_policy", ctypes.c_int32),
         ("stored_values", ctypes.c_int64),
+        ("d_a_words", ctypes.c_void_p),
+        ("d_a_packed", ctypes.c_void_p),
     ]
 
 

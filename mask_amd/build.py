@@ -81,12 +81,17 @@ GENERATED_SHAPES = ((16, 8, False), (32, 32, False), (16, 8, True))
 def build_generated_one(bm: int, bk: int, lds: bool = False) -> str:
     """Emit and compile an operator of the HIP emitter for one SR-BCRS block
     shape into mask_amd/generated/: the default strategy, or (lds) one that
-    asks for B in shared memory (materialize_b_array_ref_to_smem)."""
+    stages B in LDS with direct-to-LDS loads (b_array_ref_mode
+    "global_load_lds")."""
     from .backend_registry import sr_bcrs_spec
     from .emitter import lower_format_operator
-    strategy = {"tensor_placement": {"materialize_b_array_ref_to_smem": True}} if lds else None
-    name = f"sr_bcrs_{bm}x{bk}{'_lds' if lds else ''}.so"
-    return lower_format_operator(sr_bcrs_spec(bm, bk), GENERATED / name, strategy=strategy)["operator_path"]
+    strategy = ({"tensor_placement": {"materialize_b_array_ref_to_smem": True, "b_array_ref_mode": "global_load_lds"}}
+                if lds else None)
+    name = f"sr_bcrs_{bm}x{bk}{'_lds' if lds else ''}"
+    work = PKG / "_build" / "generated" / name
+    return lower_format_operator(format_obj=sr_bcrs_spec(bm, bk), codegen_format_name="SR_BCRS",
+                                 operator_path=GENERATED / f"{name}.so", ir_dir=work / "ir",
+                                 strategy_dir=work / "strategy", strategy_decision=strategy)["operator_path"]
 
 
 if __name__ == "__main__":

@@ -420,6 +420,11 @@ struct srbcrs_plan {
           *d_red_slot_off = nullptr;
   float* d_partial = nullptr;
   size_t partial_cap = 0;  // floats
+  // Device buffers a plan replaced (older partial buffers and task tables).
+  // They are freed only with the plan: a HIP graph captured on an earlier
+  // run may still hold their addresses, and a replay must not write freed
+  // memory.
+  std::vector<void*> retired;
   // packing (generated-operator bridge): packed rows, row map, omitted rows
   bool canonical = true;   // the preprocess_gpu conversion (edge maps available)
   int32_t packing = 0, dup_policy = 0;
@@ -438,21 +443,27 @@ struct srbcrs_plan {
   // current schedule (cleared when it changes)
   std::map<int64_t, srbcrs_run_opts> tuned;
 
-  void free_schedule() {
-    dev_free(d_group_off);
-    dev_free(d_task_begin);
-    dev_free(d_task_end);
-    dev_free(d_task_window);
-    dev_free(d_task_slot);
-    dev_free(d_red_window);
-    dev_free(d_red_slot_off);
+  template <class T>
+  void retire(T*& p) {
+    if (p) retired.push_back(static_cast<void*>(p));
+    p = nullptr;
+  }
+  void retire_schedule() {
+    retire(d_group_off);
+    retire(d_task_begin);
+    retire(d_task_end);
+    retire(d_task_window);
+    retire(d_task_slot);
+    retire(d_red_window);
+    retire(d_red_slot_off);
   }
   ~srbcrs_plan() {
     int cur = 0;
     bool switched = false;
     if (hipGetDevice(&cur) == hipSuccess && cur != device) switched = hipSetDevice(device) == hipSuccess;
-    free_schedule();
-    dev_free(d_partial);
+    retire_schedule();
+    retire(d_partial);
+    for (void* p : retired) (void)hipFree(p);
     dev_free(d_soff);
     dev_free(d_sidx);
     dev_free(d_val);
@@ -807,6 +818,8 @@ int srbcrs_plan_get(const srbcrs_plan* plan, srbcrs_plan_desc* out) {
     out->packing = plan->packing;
     out->dup_policy = plan->dup_policy;
     out->stored_values = plan->d_awords || plan->total == 0 ? plan->n_apacked : -1;
+    out->d_a_words = plan->d_awords;
+    out->d_a_packed = plan->d_apacked;
   });
 }
 
@@ -983,7 +996,7 @@ int srbcrs_plan_set_schedule(srbcrs_plan* plan, const char* policy, int32_t para
     if (cur != plan->device) fail(SRBCRS_ESTATE, "plan lives on device %d, current device is %d", plan->device, cur);
     Schedule* s = build_schedule(plan->h_soff.data(), plan->Mo, policy, param);
     std::unique_ptr<Schedule> hold(s);
-    plan->free_schedule();
+    plan->retire_schedule();
     plan->tuned.clear();
     plan->sched = std::move(*s);
     if (plan->sched.policy != "row") {
@@ -1088,10 +1101,11 @@ int srbcrs_run_ex(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int
     const Schedule& s = plan->sched;
     const size_t need = (size_t)s.n_slots * plan->blk_h * (size_t)ldc;
     if (need > plan->partial_cap) {
-      hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
-      dev_free(plan->d_partial);
-      plan->partial_cap = 0;
-      plan->d_partial = dev_alloc<float>(need);
+      // grow-only; the old buffer is retired, not freed (launches in flight
+      // and captured graphs keep a valid address), so no stream sync here
+      float* grown = dev_alloc<float>(need);
+      plan->retire(plan->d_partial);
+      plan->d_partial = grown;
       plan->partial_cap = need;
     }
     a.partial = plan->d_partial;

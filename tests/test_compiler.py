@@ -76,7 +76,8 @@ def test_select_backend_targets_and_tiles():
 
 def _strategy(**kw):
     tp = SimpleNamespace(tile_b=kw.get("tile_b", 64), b_smem_swizzle="swizzle_323",
-                         materialize_b_array_ref_to_smem=kw.get("b_smem", False))
+                         materialize_b_array_ref_to_smem=kw.get("b_smem", False),
+                         b_array_ref_mode=kw.get("b_mode", "cp_async_1x4"))
     pl = SimpleNamespace(enable_async_pipeline=kw.get("pipe", True), max_wait_prior=kw.get("mwp"),
                          stage_shifts=kw.get("shifts", []))
     rs = SimpleNamespace(execution_policy=kw.get("policy", "auto"), task_group_tiles=kw.get("tgt", 64),
@@ -101,11 +102,14 @@ def test_strategy_knob_mapping():
     assert params_from_strategy({"tensor_placement": {"tile_b": 16}}, plan).vec == 1
     p32 = params_from_strategy(None, select_backend(sr_bcrs_spec(32, 32)))
     assert (p32.blk_m, p32.blk_k, p32.col_groups) == (32, 32, 1)
-    # B placement: materialize_b_array_ref_to_smem -> LDS staging, at vec 4 only
-    assert params_from_strategy(_strategy(b_smem=True), plan).b_lds
-    assert not params_from_strategy(_strategy(b_smem=True, tile_b=32), plan).b_lds
-    assert not params_from_strategy(_strategy(), plan).b_lds
-    assert params_from_strategy({"tensor_placement": {"materialize_b_array_ref_to_smem": True}}, plan).b_lds
+    # B placement: LDS staging only for the gfx950 mode global_load_lds, at vec 4; the
+    # reference's default shared-memory staging maps to the (faster) register ring
+    assert params_from_strategy(_strategy(b_smem=True, b_mode="global_load_lds"), plan).b_lds
+    assert not params_from_strategy(_strategy(b_smem=True), plan).b_lds
+    assert not params_from_strategy(_strategy(b_smem=True, b_mode="global_load_lds", tile_b=32), plan).b_lds
+    assert not params_from_strategy(_strategy(b_mode="global_load_lds"), plan).b_lds
+    assert params_from_strategy({"tensor_placement": {"materialize_b_array_ref_to_smem": True,
+                                                      "b_array_ref_mode": "global_load_lds"}}, plan).b_lds
 
 
 def test_emitted_source_structure_and_determinism():
@@ -119,13 +123,16 @@ def test_emitted_source_structure_and_determinism():
     for needle in ("#define SPARSENE_GENERATED_TILE_B 64", "#define SPARSENE_GENERATED_SUPPORTS_TASK_MAPPING 1",
                    "#define SPARSENE_GENERATED_WAVE_SIZE 64", "#define SPARSENE_GENERATED_PIPELINE_DEPTH 4",
                    "constexpr int NNZ_HINT = 7;", '#include "srbcrs_stream.hpp"',
-                   "srbcrs::spmm_stream<Src, kBH, kBW, kVEC, kG, kWAVES, kDEPTH, srbcrs::DenseA, kBSTAGE>",
+                   "srbcrs::spmm_stream<Src, kBH, kBW, kVEC, kG, kWAVES, kDEPTH, AF, kBSTAGE>",
+                   "srbcrs::CompactA{", "srbcrs::DenseA{",
                    "constexpr int kBSTAGE = 0;",
                    'extern "C" int sparsene_generated_run(', 'extern "C" int sparsene_generated_run_tasks(',
                    'extern "C" int sparsene_generated_reduce('):
         assert needle in src, needle
     meta = json.loads(src.split('R"JSON(')[1].split(')JSON"')[0])
     assert meta["kernel_params"]["depth"] == 4 and meta["format_name"] == "SR_BCRS"
+    assert meta["kernel_parameter_order"][:5] == ["dB_val", "dC_val", "dval_len_offset", "dval_new",
+                                                  "dval_sidx_new"]
     assert meta["notes"]["ignored_knobs"]["b_smem_swizzle"] == "swizzle_323"
     assert "cp.async" not in src and "__syncwarp" not in src and "mma.sync" not in src
     assert operator_sha256(src) != operator_sha256(emit_source(KernelParams()))
@@ -157,3 +164,89 @@ def test_generated_operators_are_built():
         meta = json.loads(L.sparsene_generated_metadata().decode())
         assert meta["kernel_params"]["blk_m"] == bm and meta["target"] == "gfx950"
         assert meta["kernel_params"]["b_lds"] == lds
+
+
+# ---- the reference compiler's SR_BCRS program (tests/golden/sr_bcrs_nvir_abi.json) ----
+
+def _fixture():
+    from pathlib import Path
+    return json.loads((Path(__file__).resolve().parent / "golden" / "sr_bcrs_nvir_abi.json").read_text())
+
+
+def _program_from_fixture(entry):
+    gmem = {n: SimpleNamespace(dtype=v["dtype"], shape=v["shape"]) for n, v in entry["gmem_inouts"].items()}
+    return SimpleNamespace(name=entry["program_name"], attrs=copy.deepcopy(entry["attrs"]), gmem_inouts=gmem)
+
+
+def test_emitter_accepts_the_reference_sr_bcrs_program():
+    """The gmem interface the reference's middle end produces for SR_BCRS is
+    exactly the operand set the emitted operator's run entry takes, in the
+    reference kernel's parameter order; its strategy attributes map onto the
+    template parameters."""
+    from mask_amd.emitter import SR_BCRS_GMEM_ABI, SR_BCRS_VARLENS, check_gmem_abi
+    fx = _fixture()["programs"]
+    for key, entry in fx.items():
+        assert set(entry["gmem_inouts"]) == set(SR_BCRS_GMEM_ABI), key
+        assert tuple(entry["varlens"]) == SR_BCRS_VARLENS
+        prog = _program_from_fixture(entry)
+        check_gmem_abi(prog)
+        src = HipCodeGenerator(select_backend(sr_bcrs_spec())).dump_nvop_program(prog)
+        meta = json.loads(src.split('R"JSON(')[1].split(')JSON"')[0])
+        assert meta["kernel_parameter_order"] == entry["kernel_parameter_order"], key
+        # the run entry's first ten parameters, as declared in the source
+        decl = src.split('extern "C" int sparsene_generated_run(')[1].split(")")[0]
+        names = [a.strip().split()[-1].lstrip("*") for a in decl.split(",")][:10]
+        assert names == entry["kernel_parameter_order"], names
+    p_default = params_from_strategy(fx["default"]["attrs"]["strategy_decision"], select_backend(sr_bcrs_spec()))
+    assert (p_default.vec, p_default.depth, p_default.b_lds, p_default.schedule) == (4, 2, False, "auto")
+    p32 = params_from_strategy(fx["tile32_wait2"]["attrs"]["strategy_decision"], select_backend(sr_bcrs_spec()))
+    assert (p32.vec, p32.col_groups, p32.depth) == (2, 1, 4)
+
+
+@pytest.mark.parametrize("mutate,msg", [
+    (lambda g: g.pop("val_sidx_new"), "missing"),
+    (lambda g: g.update(extra_ptr=SimpleNamespace(dtype="int", shape="(Varlen(M))")), "unexpected"),
+    (lambda g: g.update(val_new=SimpleNamespace(dtype="half", shape=g["val_new"].shape)), "dtype"),
+    (lambda g: g.update(val_len_offset=SimpleNamespace(dtype="int", shape="(Varlen(Mo), Param(X))")), "rank"),
+])
+def test_emitter_rejects_a_mismatched_gmem_interface(mutate, msg):
+    prog = _program_from_fixture(_fixture()["programs"]["default"])
+    mutate(prog.gmem_inouts)
+    with pytest.raises(ValueError, match=msg):
+        HipCodeGenerator().dump_nvop_program(prog)
+
+
+def test_lower_format_operator_signature_and_result(tmp_path, monkeypatch):
+    """lower_format_operator takes the reference's keyword-only arguments
+    and returns its keys (generate_custom_format_operators.py:88-157)."""
+    import inspect
+    from mask_amd import emitter
+    sig = inspect.signature(emitter.lower_format_operator)
+    for name in ("format_obj", "codegen_format_name", "operator_path", "ir_dir", "strategy_dir",
+                 "strategy_decision", "specialized_parameters", "preserve_scalar_offset_divisors",
+                 "explicit_sequential_iteration", "diagnostic_program_transform"):
+        assert sig.parameters[name].kind is inspect.Parameter.KEYWORD_ONLY, name
+    compiled = []
+
+    def fake_compile(source, out_path):
+        compiled.append(out_path)
+        out_path.with_suffix(".hip").write_text(source)
+        return out_path
+    monkeypatch.setattr(emitter, "compile_operator", fake_compile)
+    seen = []
+    res = emitter.lower_format_operator(format_obj=sr_bcrs_spec(), codegen_format_name="SR_BCRS",
+                                        operator_path=tmp_path / "op.so", ir_dir=tmp_path / "ir",
+                                        strategy_dir=tmp_path / "st", strategy_decision={"pipeline": {"max_wait_prior": 3}},
+                                        specialized_parameters={"NNZ_HINT": 3},
+                                        diagnostic_program_transform=seen.append)
+    assert {"operator_sha256", "lowered_block_barriers", "strategy_decision", "gmem_inouts"} <= set(res)
+    assert res["lowered_block_barriers"] == 0 and len(seen) == 1
+    assert set(res["gmem_inouts"]) == set(_fixture()["programs"]["default"]["gmem_inouts"])
+    assert res["kernel_params"]["depth"] == 8
+    src = (tmp_path / "op.hip").read_text()
+    import hashlib
+    assert res["operator_sha256"] == hashlib.sha256(src.encode()).hexdigest()
+    assert "constexpr int NNZ_HINT = 3;" in src and (tmp_path / "ir" / "06_nvir_before_pipeline.txt").exists()
+    with pytest.raises(NotImplementedError):
+        emitter.lower_format_operator(format_obj=sr_bcrs_spec(), codegen_format_name="ME_TCF",
+                                      operator_path=tmp_path / "x.so", ir_dir=tmp_path, strategy_dir=tmp_path)

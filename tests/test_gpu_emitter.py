@@ -39,9 +39,21 @@ def test_generated_operator_matches_library(gpu, blk, lds):
         torch.cuda.synchronize()
         assert torch.equal(out, ref), pol
         assert_gate(gate(out.cpu().numpy(), rowptr, colind, values, B, M))
-    # the operator's own default ("auto") schedule
+    # "auto" means the same schedule on both paths (the library's rule), so the same bits
+    plan.set_schedule("auto", 0)
+    ref = plan.run(dB)
     auto = op.run(plan, dB)
+    torch.cuda.synchronize()
+    assert torch.equal(auto, ref)
     assert_gate(gate(auto.cpu().numpy(), rowptr, colind, values, B, M))
+    # both A sources of the operator give the library's bits
+    for a_op in ("compact", "dense"):
+        for pol, param in (("row", 0), ("split", 3)):
+            plan.set_schedule(pol, param)
+            ref = plan.run(dB, a_operand=a_op)
+            got = op.run(plan, dB, schedule=pol, schedule_param=param, a_operand=a_op)
+            torch.cuda.synchronize()
+            assert torch.equal(got, ref), (a_op, pol)
 
 
 def test_generated_operator_rejects_bad_operands(gpu):
@@ -57,3 +69,42 @@ def test_generated_operator_rejects_bad_operands(gpu):
         op.run(plan, torch.ones((K, 64), device="cuda"), schedule="row")   # 64 % 128 != 0
     with pytest.raises(RuntimeError, match="fewer rows"):
         op.run(plan, torch.ones((int(colind.max()), 128), device="cuda"), schedule="row")
+    dB = torch.ones((K, 128), device="cuda")
+    with pytest.raises(RuntimeError, match="rows, the plan writes"):
+        op.run(plan, dB, out=torch.empty((M - 1, 128), device="cuda"), schedule="row")
+    with pytest.raises(RuntimeError, match="float32"):
+        op.run(plan, dB.double(), schedule="row")
+    with pytest.raises(RuntimeError, match="CUDA tensor"):
+        op.run(plan, dB.cpu(), schedule="row")
+    with pytest.raises(RuntimeError, match="row-major"):
+        op.run(plan, torch.ones((128, K), device="cuda").t(), schedule="row")
+
+
+def test_generated_c_abi_checks_operands(gpu):
+    """The generated C entry itself refuses inconsistent operands (status -1,
+    nothing launched): a C with fewer rows than M, a wrong offsets length
+    (Mo), a half-given compact copy."""
+    import torch
+    from mask_amd.build import GENERATED
+    from mask_amd.emitter import GeneratedOperator
+    from mask_amd.SRBCRSSpMM import Plan
+    op = GeneratedOperator(GENERATED / "sr_bcrs_16x8.so")
+    M, K, N = 40, 60, 128
+    rowptr, colind, values = random_csr(M, K, 0.1, seed=2)
+    plan = Plan(*(torch.from_numpy(a).cuda() for a in (rowptr, colind, values)), M)
+    d = plan.desc
+    B = torch.ones((K, N), device="cuda")
+    C = torch.empty((M, N), device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    run = op._lib.sparsene_generated_run
+    Mo = plan.row_windows + 1
+    ok = run(B.data_ptr(), C.data_ptr(), d.d_soff, d.d_val, d.d_sidx, K, M, Mo, N, plan.total_blocks, N, N, M,
+             None, None, None, st)
+    assert ok == 0
+    assert run(B.data_ptr(), C.data_ptr(), d.d_soff, d.d_val, d.d_sidx, K, M, Mo, N, plan.total_blocks, N, N,
+               M - 1, None, None, None, st) == -1
+    assert run(B.data_ptr(), C.data_ptr(), d.d_soff, d.d_val, d.d_sidx, K, M, Mo + 1, N, plan.total_blocks, N, N,
+               M, None, None, None, st) == -1
+    assert run(B.data_ptr(), C.data_ptr(), d.d_soff, d.d_val, d.d_sidx, K, M, Mo, N, plan.total_blocks, N, N, M,
+               None, d.d_val, None, st) == -1
+    torch.cuda.synchronize()

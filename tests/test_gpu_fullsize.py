@@ -49,7 +49,7 @@ def test_full_size_workload(gpu, name, schedule):
     import torch
     from mask_amd import datasets
     from mask_amd.SRBCRSSpMM import Plan
-    m = datasets.make_config(name)
+    m = _workload(name)
     _say("full", name, m.M, m.nnz, m.N)
     B = m.dense()
     dev = torch.device("cuda", 0)
@@ -82,3 +82,79 @@ def test_full_size_workload(gpu, name, schedule):
     del plan_abs, scale, d, C12, C2
     # determinism
     assert torch.equal(plan.run(dB), C)
+
+
+_WORKLOADS = {}
+
+
+def _workload(name):
+    """Full-size workloads are generated once per test session (R-MAT takes ~20 s)."""
+    from mask_amd import datasets
+    if name not in _WORKLOADS:
+        _WORKLOADS[name] = datasets.make_config(name)
+    return _WORKLOADS[name]
+
+
+@pytest.mark.parametrize("name", ["banded-524288", "rmat-2^20", "gcn-232965"])
+def test_full_size_conversion_bit_exact(gpu, name):
+    """The default device converter (radix sort on the GPU) against the host
+    converter of the same CSR and against the oracle, byte for byte, on the
+    bench's full-size matrices: soff, sidx, the swizzled values and the edge
+    maps (the preprocess outputs of SRBCRSSpMM_kernel.cu:226-282, 343-392)."""
+    import torch
+    from mask_amd.SRBCRSSpMM import Plan
+    from tests.test_gpu_convert import _arrays, _same
+    m = _workload(name)
+    _say("full conversion", name, m.M, m.nnz)
+    t = lambda a: torch.from_numpy(a).cuda()
+    rp, ci, vv = t(m.rowptr), t(m.colind), t(m.values)
+    dev = _arrays(Plan(rp, ci, vv, m.M, convert_on="device"))
+    torch.cuda.empty_cache()
+    host = _arrays(Plan(rp, ci, vv, m.M, convert_on="host"))
+    torch.cuda.empty_cache()
+    _same(dev, host)
+    del host
+    _same(dev, oracle.convert(m.rowptr, m.colind, m.values, m.M))
+
+
+def test_full_size_gcn_two_layer_forward(gpu):
+    """The GCN workload at full size: relu(A (X W1)) at N = 256 then
+    A (H W2) at N = 64 through the drop-in srbcrs_spmm, each layer's output
+    checked against the fp64 oracle on a seeded sample of 3000 rows (the
+    layer's dense input is the GPU's own, so the check isolates the SpMM)."""
+    import torch
+    from mask_amd import external_backend_spmm as E
+    from mask_amd.gcn import gcn2_forward, glorot_weights, graph_from_csr
+    import os
+    old = os.environ.get("SPARSENE_SRBCRS_VARIANT")
+    os.environ["SPARSENE_SRBCRS_VARIANT"] = "16x8"
+    try:
+        E.reset_backend_state()
+        m = _workload("gcn-232965")
+        _say("full gcn forward", m.M, m.nnz)
+        dev = torch.device("cuda", 0)
+        g = graph_from_csr(m, 512, dev, seed=m.seed)
+        w1, w2 = glorot_weights([512, 256, 64], seed=m.seed, device=dev)
+        out = gcn2_forward(g, w1, w2, E.srbcrs_spmm)
+        xw = (g.x @ w1).contiguous()
+        h = torch.relu(E.srbcrs_spmm(*g.a, xw, m.M, 256, m.M))
+        hw = (h @ w2).contiguous()
+        torch.cuda.synchronize()
+        assert out.shape == (m.M, 64) and h.shape == (m.M, 256)
+        rows = np.sort(np.random.default_rng(5).choice(m.M, 3000, replace=False))
+        rp, ci, vv = _rows_csr(m, rows)
+        for dense, got, relu in ((xw, h, True), (hw, out, False)):
+            D = dense.cpu().numpy()
+            ref, scale = oracle.csr_spmm_f64(rp, ci, vv, D, rows.size, with_abs=True)
+            if relu:
+                ref = np.maximum(ref, 0)
+            met = oracle.error_metrics(got.cpu().numpy()[rows], ref, scale)
+            assert met["max_ratio"] <= TOL_ELEM and met["ref_gate"] and met["rel_l2"] <= 1e-6, met
+        # the forward's own output equals the step-by-step recomputation bit for bit
+        assert torch.equal(out, E.srbcrs_spmm(*g.a, hw, m.M, 64, m.M))
+    finally:
+        if old is None:
+            os.environ.pop("SPARSENE_SRBCRS_VARIANT", None)
+        else:
+            os.environ["SPARSENE_SRBCRS_VARIANT"] = old
+        E.reset_backend_state()

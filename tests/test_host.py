@@ -370,21 +370,12 @@ def test_bench_byte_model_and_traffic_lookup():
     assert bench.algorithmic_bytes(M, N, Mo, nb // 8, 0, "srbcrs", 32, 32) == \
         4 * (Mo + 1) + nb // 8 * (32 * 4 + 1024 * 4) + nb // 8 * 32 * N * 4 + M * N * 4
     assert bench.algorithmic_bytes(10, 64, 1, 1, 100, "csr") == 4 * 11 + 8 * 100 + 4 * 64 * 100 + 4 * 10 * 64
-    from pathlib import Path
-    prof = sorted(p for p in (Path(bench.ROOT) / "profiles").glob("spmm_stream_uniform-65536_N512_*.md")
-                  if "_blk" not in p.name and "traffic_bytes:" in p.read_text())
-    assert prof, "no committed uniform profile"
-    knobs = None
-    for line in prof[0].read_text().splitlines():
-        if line.startswith("knobs:"):
-            knobs = dict(kv.split("=") for kv in line.split(":", 1)[1].split())
-    assert knobs is not None
-    got = bench.measured_traffic("uniform-65536", 512, "srbcrs", knobs)
-    assert isinstance(got, int) and got > 0
-    assert bench.measured_traffic("uniform-65536", 512, "srbcrs", {**knobs, "depth": "3"}) is None
-    assert bench.measured_traffic("uniform-65536", 512, "csr", knobs) is None
-    assert bench.measured_traffic("uniform-65536", 512, "srbcrs", knobs, "32x32") is None or \
-        knobs.get("blk") == "32x32"
+    knobs = dict(bench.PUBLISHED_KNOBS["uniform-65536"], tile_b=0, b_stage="registers")
+    got = bench.measured_profile("uniform-65536", 512, "srbcrs", knobs)
+    assert got is not None and got["dram_bytes"] > 0 and got["file"].startswith("profiles/")
+    assert bench.measured_profile("uniform-65536", 512, "srbcrs", {**knobs, "depth": 3}) is None
+    assert bench.measured_profile("uniform-65536", 512, "csr", knobs) is None
+    assert bench.measured_profile("uniform-65536", 512, "srbcrs", knobs, "32x32") is None
 
 
 def test_bench_reports_the_library_default_a_operand():
@@ -434,3 +425,54 @@ def test_gcn_autograd_on_cpu_with_torch_spmm():
     assert abs(loss.item() - ref.item()) < 1e-5
     for p, w in zip(model.parameters(), ws):
         assert torch.allclose(p.grad.double(), w.grad, atol=1e-5, rtol=1e-4)
+
+
+def test_operand_checks_raise_before_any_launch():
+    """Plan.run / Plan.tune / GeneratedOperator.run validate dense and out
+    with check_operand before handing a pointer to the GPU: a host tensor,
+    a wrong dtype or a transposed view raise here, without a GPU."""
+    torch = pytest.importorskip("torch")
+    from mask_amd.SRBCRSSpMM import check_operand
+    dev = torch.device("cuda", 0)
+    with pytest.raises(RuntimeError, match="CUDA tensor"):
+        check_operand(torch.ones(4, 16), "dense", dev)
+    with pytest.raises(RuntimeError, match="torch tensor"):
+        check_operand(np.ones((4, 16), np.float32), "dense", dev)
+
+
+def test_bench_roofline_is_bounded():
+    """bench.roofline never reports a fraction above 1: bytes that imply more
+    than the HBM peak over the step time are rejected (frac null), and the
+    dataflow bytes (gathers served by the caches) are reported as a rate only."""
+    import bench
+    t = 1e-3
+    ok = bench.roofline(t, dataflow_bytes=9e9, compulsory_bytes=2e9, padded_flops=1e10,
+                        prof={"file": "p.md", "dram_bytes": 6_000_000_000, "traffic_bytes": 6_100_000_000})
+    assert ok["frac"] == 0.75 and ok["hbm_bytes"] == 6_000_000_000 and ok["dataflow_gbs"] == 9000.0
+    assert ok["compulsory_frac"] == 0.25 and ok["basis"].startswith("measured")
+    bad = bench.roofline(t, dataflow_bytes=9e9, compulsory_bytes=2e9, padded_flops=1e10,
+                         prof={"file": "p.md", "dram_bytes": 9_000_000_000, "traffic_bytes": None})
+    assert bad["frac"] is None and bad["frac_rejected"] == 1.125
+    fallback = bench.roofline(t, 9e9, 2e9, 1e10, None)
+    assert fallback["frac"] == 0.25 and fallback["basis"].startswith("compulsory")
+
+
+def test_committed_profiles_are_physical():
+    """Every committed kernel profile with measured DRAM bytes implies at most
+    the 8 TB/s HBM peak over its own kernel average, and bench.py finds the
+    profile of each published launch setting."""
+    import bench
+    from pathlib import Path
+    found = 0
+    for path in sorted((Path(bench.ROOT) / "profiles").glob("spmm_stream_*.md")):
+        fields = dict(l.split(":", 1) for l in path.read_text().splitlines()
+                      if l.startswith(("dram_bytes:", "kernel_avg_ns:")))
+        if "dram_bytes" in fields:
+            found += 1
+            gbs = int(fields["dram_bytes"]) / int(fields["kernel_avg_ns"])
+            assert gbs <= bench.HBM_PEAK_GBS, (path.name, gbs)
+    assert found >= 1
+    for name, knobs in bench.PUBLISHED_KNOBS.items():
+        k = dict(knobs, tile_b=0, b_stage="registers")
+        prof = bench.measured_profile(name, 512, "srbcrs", k)
+        assert prof is not None and prof["dram_bytes"] > 0, name
