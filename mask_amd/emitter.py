@@ -450,6 +450,17 @@ class GeneratedOperator:
         self.params = KernelParams(**self.metadata["kernel_params"])
         self._tables = {}
 
+    def _gmem(self, dense, out, desc):
+        """The five gmem pointers in the order the operator's metadata
+        declares (the reference kernel's: sorted by gmem name), looked up by
+        name so that no call site can transpose two of them."""
+        by_name = {"dB_val": dense.data_ptr(), "dC_val": out.data_ptr(), "dval_len_offset": desc.d_soff,
+                   "dval_new": desc.d_val, "dval_sidx_new": desc.d_sidx}
+        order = self.metadata["kernel_parameter_order"][:5]
+        if sorted(order) != sorted(by_name):
+            raise RuntimeError(f"operator declares gmem operands {order}, expected {sorted(by_name)}")
+        return tuple(by_name[n] for n in order)
+
     def resolve_schedule(self, plan, schedule: Optional[str] = None, schedule_param: Optional[int] = None):
         """(policy, param) a run uses.  "auto" is resolved by the library's own
         rule (srbcrs_schedule_build), so both paths pick the same schedule
@@ -507,7 +518,7 @@ class GeneratedOperator:
                                                       out.stride(0), st):
                 raise RuntimeError("generated zero-fill failed")
         if pol == "row":
-            rc = self._lib.sparsene_generated_run(dense.data_ptr(), out.data_ptr(), d.d_soff, d.d_sidx, d.d_val,
+            rc = self._lib.sparsene_generated_run(*self._gmem(dense, out, d),
                                                   K, P, Mo, N, plan.total_blocks, dense.stride(0), out.stride(0),
                                                   out.shape[0], d.d_row_map, aw, ap, st)
             if rc:
@@ -523,7 +534,7 @@ class GeneratedOperator:
             raise RuntimeError("task-mapped runs need a dense-packed output")
         partial = torch.empty((max(tab["n_slots"], 1) * plan.blk_h, N), dtype=torch.float32, device=dense.device)
         rc = self._lib.sparsene_generated_run_tasks(
-            dense.data_ptr(), out.data_ptr(), d.d_soff, d.d_val, d.d_sidx, dev["task_begin"].data_ptr(),
+            *self._gmem(dense, out, d), dev["task_begin"].data_ptr(),
             dev["task_end"].data_ptr(), dev["task_window"].data_ptr(), dev["task_slot"].data_ptr(),
             dev["group_off"].data_ptr(), K, P, Mo, N, plan.total_blocks, tab["group_off"].size - 1,
             partial.data_ptr(), dense.stride(0), N, out.shape[0], d.d_row_map, aw, ap, st)

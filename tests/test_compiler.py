@@ -250,3 +250,21 @@ def test_lower_format_operator_signature_and_result(tmp_path, monkeypatch):
     with pytest.raises(NotImplementedError):
         emitter.lower_format_operator(format_obj=sr_bcrs_spec(), codegen_format_name="ME_TCF",
                                       operator_path=tmp_path / "x.so", ir_dir=tmp_path, strategy_dir=tmp_path)
+
+
+def test_generated_operator_passes_gmem_pointers_in_declared_order():
+    """GeneratedOperator hands the five gmem pointers to the generated entry
+    in the order the operator declares (dB_val, dC_val, dval_len_offset,
+    dval_new, dval_sidx_new): values before column indices.  A transposed
+    pair makes the kernel read block values as B-row indices."""
+    from mask_amd.build import GENERATED
+    from mask_amd.emitter import GeneratedOperator
+    so = GENERATED / "sr_bcrs_16x8.so"
+    if not so.exists():
+        pytest.skip("generated operators not built")
+    op = GeneratedOperator(so)
+    t = lambda p: SimpleNamespace(data_ptr=lambda: p)
+    desc = SimpleNamespace(d_soff=3, d_val=4, d_sidx=5)
+    assert op._gmem(t(1), t(2), desc) == (1, 2, 3, 4, 5)
+    assert op.metadata["kernel_parameter_order"][:5] == ["dB_val", "dC_val", "dval_len_offset", "dval_new",
+                                                         "dval_sidx_new"]
