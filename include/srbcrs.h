@@ -14,6 +14,7 @@
 #ifndef MASK_AMD_SRBCRS_H
 #define MASK_AMD_SRBCRS_H
 
+#include <stddef.h>
 #include <stdint.h>
 
 #ifdef __cplusplus
@@ -275,6 +276,24 @@ typedef struct srbcrs_run_opts {
 int srbcrs_run_ex(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int64_t ldb,
                   float *d_C, int64_t ldc, int64_t c_rows, const srbcrs_run_opts *opts,
                   void *stream);
+
+/* srbcrs_run_ex that allocates nothing (no hipMalloc / hipFree, no
+ * allocating library call).  No counterpart in the reference: it is for
+ * callers that cannot allocate (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid it).  The split / strict_lb / multi_bind
+ * schedules keep their partial tiles in a fixed device array of
+ * srbcrs_noalloc_scratch_floats() floats (64 MiB) that each GPU the library
+ * runs on holds until the process ends; a run whose partial tiles need more
+ * (slots x blk_h x ldc floats) is rejected with SRBCRS_EINVAL.  The "row"
+ * schedule needs no scratch.  All calls on one GPU share that array, so calls
+ * that overlap on one GPU (other streams, other threads) race; calls in
+ * stream order do not.  Results are bit-identical to srbcrs_run_ex with the
+ * same arguments.  The plan's schedule tables must exist already
+ * (srbcrs_plan_set_schedule allocates them). */
+int srbcrs_run_noalloc(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int64_t ldb,
+                       float *d_C, int64_t ldc, int64_t c_rows, const srbcrs_run_opts *opts,
+                       void *stream);
+size_t srbcrs_noalloc_scratch_floats(void);
 
 /* Time candidate launch settings on this plan for a dense width N and keep
  * one.  Candidates, in preference order: for the compact A operand (16x8

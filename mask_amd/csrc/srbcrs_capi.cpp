@@ -13,6 +13,7 @@
 #include <string>
 #include <thread>
 #include <map>
+#include <mutex>
 #include <vector>
 
 #include "../../include/srbcrs.h"
@@ -1016,10 +1017,12 @@ int srbcrs_run(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int64_
   return srbcrs_run_ex(plan, d_B, K, N, ldb, d_C, ldc, c_rows, nullptr, stream);
 }
 
-int srbcrs_run_ex(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int64_t ldb,
-                  float* d_C, int64_t ldc, int64_t c_rows, const srbcrs_run_opts* opts,
-                  void* stream) {
-  return guarded([&] {
+// The body of srbcrs_run_ex / srbcrs_run_noalloc.  fixed_partial (with room
+// for fixed_cap floats) replaces the plan's grown partial buffer; with it the
+// run allocates nothing.
+static void run_impl(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int64_t ldb, float* d_C,
+                     int64_t ldc, int64_t c_rows, const srbcrs_run_opts* opts, void* stream,
+                     float* fixed_partial, size_t fixed_cap) {
     srbcrs_run_opts tuned_opts;
     if (plan && (!opts || all_default(*opts))) {
       const auto it = plan->tuned.find(N);
@@ -1100,24 +1103,87 @@ int srbcrs_run_ex(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int
     }
     const Schedule& s = plan->sched;
     const size_t need = (size_t)s.n_slots * plan->blk_h * (size_t)ldc;
-    if (need > plan->partial_cap) {
-      // grow-only; the old buffer is retired, not freed (launches in flight
-      // and captured graphs keep a valid address), so no stream sync here
-      float* grown = dev_alloc<float>(need);
-      plan->retire(plan->d_partial);
-      plan->d_partial = grown;
-      plan->partial_cap = need;
+    float* partial = fixed_partial;
+    if (fixed_partial) {
+      if (need > fixed_cap)
+        fail(SRBCRS_EINVAL,
+             "the schedule's partial tiles need %zu floats (%d slots x %d rows x ldc %lld), above the "
+             "%zu-float scratch of srbcrs_run_noalloc; use srbcrs_run_ex or a schedule with fewer slots",
+             need, s.n_slots, plan->blk_h, (long long)ldc, fixed_cap);
+    } else {
+      if (need > plan->partial_cap) {
+        // grow-only; the old buffer is retired, not freed (launches in flight
+        // and captured graphs keep a valid address), so no stream sync here
+        float* grown = dev_alloc<float>(need);
+        plan->retire(plan->d_partial);
+        plan->d_partial = grown;
+        plan->partial_cap = need;
+      }
+      partial = plan->d_partial;
     }
-    a.partial = plan->d_partial;
+    a.partial = partial;
     srbcrs::TaskTable tt{plan->d_group_off, plan->d_task_begin, plan->d_task_end, plan->d_task_window,
                          plan->d_task_slot, (int)s.group_off.size() - 1};
     hip_check(srbcrs::launch_tasks(a, tt, vec, ro, st), "launch spmm_stream(tasks)");
-    srbcrs::ReduceArgs ra{plan->d_partial, d_C, plan->d_red_window, plan->d_red_slot_off,
+    srbcrs::ReduceArgs ra{partial, d_C, plan->d_red_window, plan->d_red_slot_off,
                           (int)s.red_window.size(), plan->blk_h, (int)plan->packed_rows, (int)N, ldc,
                           plan->d_rowmap};
     hip_check(srbcrs::launch_reduce(ra, vec, st), "launch segment_reduce");
+}
+
+int srbcrs_run_ex(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int64_t ldb,
+                  float* d_C, int64_t ldc, int64_t c_rows, const srbcrs_run_opts* opts,
+                  void* stream) {
+  return guarded([&] { run_impl(plan, d_B, K, N, ldb, d_C, ldc, c_rows, opts, stream, nullptr, 0); });
+}
+
+// ---- srbcrs_run_noalloc: partial tiles in a fixed device array ------------
+//
+// For callers that cannot allocate.  The split schedules' partial tiles go to
+// `scratch`, a file-scope device array every GPU holds from the library's
+// load until the process ends; nothing is allocated per call.  In host code
+// `scratch` names a host-side stand-in, not device memory: its device address
+// comes from hipGetSymbolAddress, once per device with that device current,
+// and only that address is handed to kernels.  Calls on one GPU share the
+// array (the last call's partial tiles stay in it); calls that overlap on one
+// GPU race.  No clearing is needed: each partial slot is written whole by its
+// task before the reduction reads it.
+namespace {
+constexpr size_t kNoallocScratchFloats = size_t(16) << 20;   // 64 MiB
+constexpr int kMaxDevices = 64;
+}  // namespace
+
+static __device__ __align__(256) float scratch[kNoallocScratchFloats];
+
+namespace {
+std::mutex g_scratch_mu;
+float* g_scratch_addr[kMaxDevices] = {};
+
+// The device address of `scratch` on the current device (looked up once per device).
+static float* noalloc_scratch() {
+  int dev = 0;
+  hip_check(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) fail(SRBCRS_ESTATE, "device %d beyond the %d the library tracks", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_addr[dev]) {
+    void* addr = nullptr;
+    hip_check(hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (!addr) fail(SRBCRS_EHIP, "hipGetSymbolAddress returned no address for the scratch array");
+    g_scratch_addr[dev] = static_cast<float*>(addr);
+  }
+  return g_scratch_addr[dev];
+}
+}  // namespace
+
+int srbcrs_run_noalloc(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int64_t ldb, float* d_C,
+                       int64_t ldc, int64_t c_rows, const srbcrs_run_opts* opts, void* stream) {
+  return guarded([&] {
+    float* partial = noalloc_scratch();
+    run_impl(plan, d_B, K, N, ldb, d_C, ldc, c_rows, opts, stream, partial, kNoallocScratchFloats);
   });
 }
+
+size_t srbcrs_noalloc_scratch_floats(void) { return kNoallocScratchFloats; }
 
 int srbcrs_plan_tune(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int64_t ldb, float* d_C,
                      int64_t ldc, int64_t c_rows, int32_t reps, srbcrs_run_opts* best, void* stream) {
