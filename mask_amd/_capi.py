@@ -11,7 +11,11 @@ from pathlib import Path
 
 import numpy as np
 
-LIB_PATH = Path(__file__).resolve().parent / "libmask_srbcrs.so"
+import os as _os
+
+# MASK_AMD_SRBCRS_LIB selects another build of the same library (the host
+# sanitizer build of mask_amd.build --sanitize); default: the in-tree one.
+LIB_PATH = Path(_os.environ.get("MASK_AMD_SRBCRS_LIB") or Path(__file__).resolve().parent / "libmask_srbcrs.so")
 
 SRBCRS_OK = 0
 SRBCRS_EINVAL = -1

@@ -94,5 +94,41 @@ def build_generated_one(bm: int, bk: int, lds: bool = False) -> str:
                                  strategy_dir=work / "strategy", strategy_decision=strategy)["operator_path"]
 
 
+SANITIZE_DIR = PKG / "_build" / "sanitize"
+SANITIZE_LIB = SANITIZE_DIR / "libmask_srbcrs_sanitize.so"
+# host-pass only: each -fsanitize goes right after -Xarch_host (GPU code is
+# not instrumented)
+SANITIZE_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+                  "-Xarch_host", "-fno-sanitize-recover=undefined", "-Xarch_host", "-fno-omit-frame-pointer",
+                  "-Xarch_host", "-g"]
+
+
+def build_sanitized() -> Path:
+    """The same library with AddressSanitizer and UndefinedBehaviorSanitizer
+    in its host code (converter, packings, row orders, schedules, plan
+    bookkeeping), for CPU tests: tests/sanitize_host.sh loads it in place of
+    the product library."""
+    from concurrent.futures import ThreadPoolExecutor
+    hipcc = _hipcc()
+    SANITIZE_DIR.mkdir(parents=True, exist_ok=True)
+
+    def compile_obj(src):
+        obj = SANITIZE_DIR / (src.rsplit(".", 1)[0] + ".o")
+        _run([hipcc, *DEVICE_FLAGS, *SANITIZE_FLAGS, f"-I{ROOT / 'include'}", "-x", "hip", "-c", str(CSRC / src),
+              "-o", str(obj)])
+        return str(obj)
+
+    with ThreadPoolExecutor(max_workers=6) as ex:
+        objs = list(ex.map(compile_obj, ("srbcrs_stream_compact.hip", "srbcrs_stream_dense.hip", "srbcrs_kernels.hip",
+                                         "srbcrs_capi.cpp", "srbcrs_pack.cpp", "srbcrs_convert.hip",
+                                         "srbcrs_compact.hip")))
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-shared-libasan", "-fsanitize=address,undefined",
+          "-o", str(SANITIZE_LIB), *objs, "-lpthread"])
+    return SANITIZE_LIB
+
+
 if __name__ == "__main__":
-    print(build(verbose="-v" in sys.argv))
+    if "--sanitize" in sys.argv:
+        print(build_sanitized())
+    else:
+        print(build(verbose="-v" in sys.argv))
