@@ -85,6 +85,33 @@ def copy_calibration(mib):
     print(json.dumps({"copy_calibration_bytes_read": n * 4, "copy_calibration_bytes_written": n * 4}))
 
 
+def copy_bandwidth(mib=1024, reps=20):
+    """What plain streaming kernels move on this box, as context for the
+    SpMM's HBM-side rate (HIP events, mib MiB buffers): torch's copy (read +
+    write, the read/write mix of an SpMM that writes C), a read-only sum and
+    a write-only fill.  GB/s of bytes moved."""
+    import torch
+    n = mib * (1 << 20) // 4
+    a = torch.ones(n, dtype=torch.float32, device="cuda")
+    b = torch.empty_like(a)
+    out = {}
+    for name, fn, nbytes in (("copy", lambda: b.copy_(a), 2 * n * 4), ("read", lambda: a.sum(), n * 4),
+                             ("write", lambda: b.fill_(2.0), n * 4)):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+        e[0].record()
+        for _ in range(reps):
+            fn()
+        e[1].record()
+        torch.cuda.synchronize()
+        out[name] = round(nbytes * reps / (e[0].elapsed_time(e[1]) / 1e3) / 1e9, 1)
+    del a, b
+    torch.cuda.empty_cache()
+    return out
+
+
 def gcn_forward_bench(args):
     """The GCN workload's two-layer forward relu(A (X W1)) -> A (H W2) on
     one GPU: SpMM at N = 256 and N = 64 (SR-BCRS 16x8, split schedule) plus
@@ -313,7 +340,7 @@ def algorithmic_bytes(M, N, Mo, nb, nnz, kernel, bh=16, bw=8):
 # --tune times the candidates on the box instead.
 PUBLISHED_KNOBS = {
     "uniform-65536": {"depth": 4, "wg_cols": 128, "grid_order": 3, "windows_per_wave": 1, "a_operand": "compact"},
-    "banded-524288": {"depth": 2, "wg_cols": 128, "grid_order": 1, "windows_per_wave": 1, "a_operand": "dense"},
+    "banded-524288": {"depth": 4, "wg_cols": 128, "grid_order": 1, "windows_per_wave": 1, "a_operand": "dense"},
     "rmat-2^20": {"depth": 4, "wg_cols": 64, "grid_order": 3, "windows_per_wave": 1, "a_operand": "compact"},
 }
 # the second north-star configuration, measured in the same invocation as the headline
@@ -341,12 +368,20 @@ def main():
         return
 
     result = measure(args, args.config, mtx=args.mtx)
+    streams = copy_bandwidth()
+    copy_gbs = streams["copy"]
+    result["roofline"]["stream_gbs"] = streams
+    if result["roofline"].get("frac") is not None:
+        result["roofline"]["frac_of_copy"] = round(result["roofline"]["achieved"] / copy_gbs, 4)
     default_run = (args.config == "uniform-65536" and not args.mtx and not args.extra_off and args.N in (None, 512)
                    and args.kernel == "srbcrs" and args.blk == "16x8" and args.row_order == "identity")
     if default_run:
         result["extra_configs"] = {}
         for name in EXTRA_CONFIGS:
             extra = measure(args, name, cpu_seconds=max(3.0, args.cpu_seconds / 2))
+            extra["roofline"]["stream_gbs"] = streams
+            if extra["roofline"].get("frac") is not None:
+                extra["roofline"]["frac_of_copy"] = round(extra["roofline"]["achieved"] / copy_gbs, 4)
             result["extra_configs"][name] = {k: extra[k] for k in (
                 "value", "unit", "ms_per_step", "ms_per_step_median", "config", "roofline", "parity",
                 "cpu_baseline") if k in extra}
