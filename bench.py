@@ -85,28 +85,33 @@ def copy_calibration(mib):
     print(json.dumps({"copy_calibration_bytes_read": n * 4, "copy_calibration_bytes_written": n * 4}))
 
 
-def copy_bandwidth(mib=1024, reps=20):
+def copy_bandwidth(mib=2048, reps=10):
     """What plain streaming kernels move on this box, as context for the
-    SpMM's HBM-side rate (HIP events, mib MiB buffers): torch's copy (read +
-    write, the read/write mix of an SpMM that writes C), a read-only sum and
-    a write-only fill.  GB/s of bytes moved."""
+    SpMM's HBM-side rate: the library's float4 grid-stride probes
+    (srbcrs_stream_probe) over mib MiB buffers -- copy (read + write, the mix
+    of an SpMM that writes C), read-only, write-only -- each at a few grid
+    sizes, best kept, HIP events on the launch stream.  GB/s of bytes moved."""
     import torch
+    from mask_amd import _capi
+    L = _capi.lib()
     n = mib * (1 << 20) // 4
     a = torch.ones(n, dtype=torch.float32, device="cuda")
     b = torch.empty_like(a)
+    st = torch.cuda.current_stream().cuda_stream
     out = {}
-    for name, fn, nbytes in (("copy", lambda: b.copy_(a), 2 * n * 4), ("read", lambda: a.sum(), n * 4),
-                             ("write", lambda: b.fill_(2.0), n * 4)):
-        for _ in range(3):
-            fn()
-        torch.cuda.synchronize()
-        e = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
-        e[0].record()
-        for _ in range(reps):
-            fn()
-        e[1].record()
-        torch.cuda.synchronize()
-        out[name] = round(nbytes * reps / (e[0].elapsed_time(e[1]) / 1e3) / 1e9, 1)
+    for kind, name, mult in ((0, "copy", 2), (1, "read", 1), (2, "write", 1)):
+        best = 0.0
+        for blocks in (1024, 4096, 65536):
+            for _ in range(2):
+                _capi.check(L.srbcrs_stream_probe(kind, a.data_ptr(), b.data_ptr(), n, blocks, st))
+            e = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+            e[0].record()
+            for _ in range(reps):
+                _capi.check(L.srbcrs_stream_probe(kind, a.data_ptr(), b.data_ptr(), n, blocks, st))
+            e[1].record()
+            torch.cuda.synchronize()
+            best = max(best, mult * n * 4 * reps / (e[0].elapsed_time(e[1]) / 1e3) / 1e9)
+        out[name] = round(best, 1)
     del a, b
     torch.cuda.empty_cache()
     return out

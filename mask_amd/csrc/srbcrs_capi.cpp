@@ -1185,6 +1185,20 @@ int srbcrs_run_noalloc(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N
 
 size_t srbcrs_noalloc_scratch_floats(void) { return kNoallocScratchFloats; }
 
+int srbcrs_stream_probe(int32_t kind, const float* d_a, float* d_b, int64_t n_floats, int32_t blocks,
+                        void* stream) {
+  return guarded([&] {
+    if (kind < 0 || kind > 2) fail(SRBCRS_EINVAL, "kind must be 0 (copy), 1 (read) or 2 (write)");
+    if (n_floats < 0 || n_floats % 4) fail(SRBCRS_EINVAL, "n_floats must be a non-negative multiple of 4");
+    if (blocks < 1 || blocks > (1 << 20)) fail(SRBCRS_EINVAL, "blocks must be in [1, 2^20]");
+    if ((kind != 2 && !d_a) || !d_b) fail(SRBCRS_EINVAL, "buffer is NULL");
+    if ((reinterpret_cast<uintptr_t>(d_a) | reinterpret_cast<uintptr_t>(d_b)) % 16)
+      fail(SRBCRS_EINVAL, "buffers must be 16-byte aligned");
+    hip_check(srbcrs::launch_stream_probe(kind, d_a, d_b, n_floats / 4, blocks, static_cast<hipStream_t>(stream)),
+              "launch stream probe");
+  });
+}
+
 int srbcrs_plan_tune(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int64_t ldb, float* d_C,
                      int64_t ldc, int64_t c_rows, int32_t reps, srbcrs_run_opts* best, void* stream) {
   if (!plan) return guarded([] { fail(SRBCRS_EINVAL, "plan is NULL"); });

@@ -79,5 +79,7 @@ hipError_t launch_tasks_compact(const StreamArgs& a, const TaskTable& t, int vec
 hipError_t launch_reduce(const ReduceArgs& a, int vec, hipStream_t st);
 hipError_t launch_csr(const CsrArgs& a, int vec, hipStream_t st);
 hipError_t launch_zero_rows(float* C, const int* rows, int n_rows, int N, int64_t ldc, hipStream_t st);
+// Streaming-rate probes (kind 0 copy a -> b, 1 read a, 2 write b), n4 float4 elements.
+hipError_t launch_stream_probe(int kind, const float* a, float* b, int64_t n4, int blocks, hipStream_t st);
 
 }  // namespace srbcrs
