@@ -184,3 +184,34 @@ def test_32x32_knobs_and_schedules(gpu):
     for pol in (("split", 0), ("split", 2), ("strict_lb", 5), ("multi_bind", 0)):
         plan.set_schedule(*pol)
         assert_gate(gate(plan.run(dB).cpu().numpy(), rowptr, colind, values, B, M))
+
+
+def test_base_variant_runs_on_a_16x8_plan(gpu, monkeypatch):
+    """run_SRBCRS (32x32 preprocess) executes on a 16x8 plan of the same CSR
+    by default -- within the gate, and bit-equal to the 16x8 plan's own run --
+    and on the 32x32 blocks themselves with SPARSENE_SRBCRS_BASE_NATIVE=1
+    (bit-equal to the 32x32 plan's run).  The preprocess outputs stay the
+    32x32 arrays either way."""
+    import torch
+    from mask_amd import SRBCRSSpMM as S
+    M, K, N = 300, 500, 128
+    rowptr, colind, values = random_csr(M, K, 0.03, seed=77, heavy_rows=2, heavy_len=400)
+    B = np.random.default_rng(77).uniform(-1, 1, (K, N)).astype(np.float32)
+    ci, rp, vv = _dev_csr(rowptr, colind, values)
+    z = torch.zeros(1, dtype=torch.int32, device="cuda")
+    rwo, _, tid, toff, a2x, total = S.preprocess_gpu(ci, rp, vv, M, 32, 32, z, z, z)
+    assert total == oracle.convert(rowptr, colind, values, M, 32, 32)["total"]
+    dB = torch.from_numpy(B).cuda()
+    _say("base variant execution", M, N)
+    monkeypatch.delenv("SPARSENE_SRBCRS_BASE_NATIVE", raising=False)
+    (fast,) = S.run_SRBCRS(dB, rwo, tid, toff, a2x, M, colind.size, "row")
+    entry = S._cache[int(rwo.data_ptr())]
+    assert entry.exec_plan is not None and (entry.exec_plan.blk_h, entry.exec_plan.blk_w) == (16, 8)
+    p16 = S.Plan(rp, ci, vv, M, 16, 8)
+    assert torch.equal(fast, p16.run(dB))
+    assert_gate(gate(fast.cpu().numpy(), rowptr, colind, values, B, M))
+    monkeypatch.setenv("SPARSENE_SRBCRS_BASE_NATIVE", "1")
+    (native,) = S.run_SRBCRS(dB, rwo, tid, toff, a2x, M, colind.size, "row")
+    p32 = S.Plan(rp, ci, vv, M, 32, 32)
+    assert torch.equal(native, p32.run(dB))
+    assert_gate(gate(native.cpu().numpy(), rowptr, colind, values, B, M))
