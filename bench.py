@@ -379,6 +379,7 @@ def main():
     if result["roofline"].get("frac") is not None:
         result["roofline"]["frac_of_copy"] = round(result["roofline"]["achieved"] / copy_gbs, 4)
     default_run = (args.config == "uniform-65536" and not args.mtx and not args.extra_off and args.N in (None, 512)
+                   and not explicit_knobs(args)
                    and args.kernel == "srbcrs" and args.blk == "16x8" and args.row_order == "identity")
     if default_run:
         result["extra_configs"] = {}

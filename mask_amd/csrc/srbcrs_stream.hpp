@@ -356,6 +356,20 @@ __device__ __forceinline__ void store_tile(const f4 (&acc)[G][VEC], float* __res
 // `slot` for the segment reduction.  A group is a run of consecutive tasks
 // with contiguous block ranges, processed by one wave per column chunk.
 
+// An int at p[i] for a wave-uniform i, read through the constant address
+// space so that the compiler emits a scalar load (counted on lgkmcnt).  Task
+// metadata is read this way: as a vector load it would be counted on vmcnt
+// with the B ring, and the wait for it at a task boundary would drain every
+// B load in flight.
+__device__ __forceinline__ int uniform_load(const int* __restrict__ p, int64_t i) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  typedef const __attribute__((address_space(4))) int cint;
+  return ((cint*)p)[i];
+#else
+  return p[i];
+#endif
+}
+
 // Row schedule: task t = row window t, groups of `wpw` consecutive windows.
 struct RowTasks {
   const int* __restrict__ soff;
@@ -366,8 +380,8 @@ struct RowTasks {
     t0 = g * wpw;
     t1 = t0 + wpw < Mo ? t0 + wpw : Mo;
   }
-  __device__ __forceinline__ int64_t begin(int t) const { return soff[t]; }
-  __device__ __forceinline__ int64_t end(int t) const { return soff[t + 1]; }
+  __device__ __forceinline__ int64_t begin(int t) const { return uniform_load(soff, t); }
+  __device__ __forceinline__ int64_t end(int t) const { return uniform_load(soff, t + 1); }
   __device__ __forceinline__ int window(int t) const { return t; }
   __device__ __forceinline__ int slot(int) const { return -1; }
 };
@@ -381,13 +395,13 @@ struct TableTasks {
   const int* __restrict__ task_slot;
   const int* __restrict__ rowmap = nullptr;   // packed row -> output row (null = identity)
   __device__ __forceinline__ void group(int g, int& t0, int& t1) const {
-    t0 = group_off[g];
-    t1 = group_off[g + 1];
+    t0 = uniform_load(group_off, g);
+    t1 = uniform_load(group_off, g + 1);
   }
-  __device__ __forceinline__ int64_t begin(int t) const { return task_begin[t]; }
-  __device__ __forceinline__ int64_t end(int t) const { return task_end[t]; }
-  __device__ __forceinline__ int window(int t) const { return task_window[t]; }
-  __device__ __forceinline__ int slot(int t) const { return task_slot[t]; }
+  __device__ __forceinline__ int64_t begin(int t) const { return uniform_load(task_begin, t); }
+  __device__ __forceinline__ int64_t end(int t) const { return uniform_load(task_end, t); }
+  __device__ __forceinline__ int window(int t) const { return uniform_load(task_window, t); }
+  __device__ __forceinline__ int slot(int t) const { return uniform_load(task_slot, t); }
 };
 
 template <class Src, int BH, int VEC, int G>
@@ -530,25 +544,42 @@ __global__ __launch_bounds__(64 * WAVES) void spmm_stream(
       idx[d].load(sidx, nu);
       am[d] = asrc.template meta<BH, BW>(nu, lane);
     }
-    for (int64_t base = us; base < ue; base += DEPTH) {
+    // Steady state: while a unit lies beyond this round, every slot is
+    // refilled after its MFMAs, unconditionally (a refill past the last unit
+    // reloads the last unit: at most DEPTH - 1 duplicate loads per wave).
+    // With the same loads on every path through the loop body the compiler
+    // counts the younger loads exactly and waits only for the slot it is
+    // about to use; conditional refills gave it paths with fewer loads and
+    // made it wait for the whole ring (vmcnt(0)) once per round.
+    int64_t base = us;
+    for (; base + DEPTH < ue; base += DEPTH) {
 #pragma unroll
       for (int d = 0; d < DEPTH; ++d) {
         const int64_t u = base + d;
-        if (u < ue) {
-          while (u >= tend) {   // crossed into the next task (empty tasks flush zeros)
-            flush_task<Src, BH, VEC, G>(src, t, acc, C, partial, M, ldc, col0, lane);
-            ++t;
-            tend = src.end(t) * S::Q;
-          }
-          mma_frag<S::H, VEC, G>(f[d], acc);
+        while (u >= tend) {   // crossed into the next task (empty tasks flush zeros)
+          flush_task<Src, BH, VEC, G>(src, t, acc, C, partial, M, ldc, col0, lane);
+          ++t;
+          tend = src.end(t) * S::Q;
         }
-        const int64_t nu = u + DEPTH;
-        if (nu < ue) {
-          load_frag<BH, BW, VEC, G>(f[d], B, asrc, nu, idx[d].pick(k), am[d], a_off, ldb, col0, lane);
-          const int64_t nn = nu + DEPTH < last ? nu + DEPTH : last;
-          idx[d].load(sidx, nn);
-          am[d] = asrc.template meta<BH, BW>(nn, lane);
+        mma_frag<S::H, VEC, G>(f[d], acc);
+        const int64_t nu = u + DEPTH < last ? u + DEPTH : last;
+        load_frag<BH, BW, VEC, G>(f[d], B, asrc, nu, idx[d].pick(k), am[d], a_off, ldb, col0, lane);
+        const int64_t nn = nu + DEPTH < last ? nu + DEPTH : last;
+        idx[d].load(sidx, nn);
+        am[d] = asrc.template meta<BH, BW>(nn, lane);
+      }
+    }
+    // Drain: the last round's units are in the ring; nothing more to load.
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d) {
+      const int64_t u = base + d;
+      if (u < ue) {
+        while (u >= tend) {
+          flush_task<Src, BH, VEC, G>(src, t, acc, C, partial, M, ldc, col0, lane);
+          ++t;
+          tend = src.end(t) * S::Q;
         }
+        mma_frag<S::H, VEC, G>(f[d], acc);
       }
     }
     }
