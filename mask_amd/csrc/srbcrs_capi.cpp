@@ -1231,7 +1231,7 @@ int srbcrs_plan_tune(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
       // several consecutive windows per wave: fewer waves than resident
       // slots, all sweeping their windows' columns in step
       for (int32_t wpw : {4, 8})
-        for (int32_t depth : {4, 8}) {
+        for (int32_t depth : {2, 4, 8}) {
           srbcrs_run_opts o{};
           o.depth = depth;
           o.wg_cols = 128;
