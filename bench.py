@@ -344,8 +344,8 @@ def algorithmic_bytes(M, N, Mo, nb, nnz, kernel, bh=16, bw=8):
 # every run times the same kernel instantiation as the committed rocprofv3 profile of that workload;
 # --tune times the candidates on the box instead.
 PUBLISHED_KNOBS = {
-    "uniform-65536": {"depth": 2, "wg_cols": 128, "grid_order": 1, "windows_per_wave": 8, "a_operand": "compact"},
-    "banded-524288": {"depth": 2, "wg_cols": 128, "grid_order": 1, "windows_per_wave": 1, "a_operand": "dense"},
+    "uniform-65536": {"depth": 2, "wg_cols": 256, "grid_order": 1, "windows_per_wave": 8, "a_operand": "compact"},
+    "banded-524288": {"depth": 2, "wg_cols": 256, "grid_order": 1, "windows_per_wave": 1, "a_operand": "dense"},
     "rmat-2^20": {"depth": 4, "wg_cols": 64, "grid_order": 3, "windows_per_wave": 1, "a_operand": "compact"},
 }
 # the second north-star configuration, measured in the same invocation as the headline

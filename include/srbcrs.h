@@ -224,7 +224,10 @@ int srbcrs_run(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int64_
  *   wg_cols      columns per workgroup, a power of two in 64..512
  *                (0 = 128); 32x32 blocks run 128-column waves (two
  *                64-column groups per lane) in workgroups of 256 columns
- *                or more, 64-column waves below;
+ *                or more, 64-column waves below; 16x8 blocks run
+ *                256-column waves (four groups per lane, N % 256 == 0) in
+ *                workgroups of 256 columns or more, 128-column waves at 128,
+ *                64-column waves at 64;
  *   grid_order   0 = default (chunk-major), 1 = chunk-major: one column
  *                chunk of every window before the next chunk (narrower B
  *                working set per XCD), 2 = window-major, 3 = chunk sweep:

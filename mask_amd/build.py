@@ -127,8 +127,47 @@ def build_sanitized() -> Path:
     return SANITIZE_LIB
 
 
+# Decomposition builds: the same library with one part of the SpMM's work taken
+# out, for timing only (their results are wrong on purpose and nothing but a
+# measurement loads them, through MASK_AMD_SRBCRS_LIB).
+EXPERIMENTS = {
+    "no_a": "SRBCRS_EXPERIMENT_NO_A",                  # dense A fragments not loaded
+    "no_b": "SRBCRS_EXPERIMENT_NO_B",                  # B rows not gathered
+    "no_mfma": "SRBCRS_EXPERIMENT_NO_MFMA",            # one VALU FMA per MFMA instead
+    "plain_c_store": "SRBCRS_EXPERIMENT_PLAIN_C_STORE",  # C written with plain (not nontemporal) stores
+}
+
+
+def build_experiment(name: str) -> Path:
+    """mask_amd/experiments/libmask_srbcrs_<name>.so with the macro of
+    EXPERIMENTS[name] defined (objects under mask_amd/_build)."""
+    from concurrent.futures import ThreadPoolExecutor
+    macro = EXPERIMENTS[name]
+    hipcc = _hipcc()
+    out_dir = PKG / "_build" / "experiments" / name
+    out_dir.mkdir(parents=True, exist_ok=True)
+
+    def compile_obj(src):
+        obj = out_dir / (src.rsplit(".", 1)[0] + ".o")
+        _run([hipcc, *DEVICE_FLAGS, f"-D{macro}=1", f"-I{ROOT / 'include'}", "-x", "hip", "-c", str(CSRC / src),
+              "-o", str(obj)])
+        return str(obj)
+
+    with ThreadPoolExecutor(max_workers=6) as ex:
+        objs = list(ex.map(compile_obj, ("srbcrs_stream_compact.hip", "srbcrs_stream_dense.hip", "srbcrs_kernels.hip",
+                                         "srbcrs_capi.cpp", "srbcrs_pack.cpp", "srbcrs_convert.hip",
+                                         "srbcrs_compact.hip")))
+    lib_dir = PKG / "experiments"
+    lib_dir.mkdir(exist_ok=True)
+    lib = lib_dir / f"libmask_srbcrs_{name}.so"
+    _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(lib), *objs, "-lpthread"])
+    return lib
+
+
 if __name__ == "__main__":
-    if "--sanitize" in sys.argv:
+    if "--experiment" in sys.argv:
+        print(build_experiment(sys.argv[sys.argv.index("--experiment") + 1]))
+    elif "--sanitize" in sys.argv:
         print(build_sanitized())
     else:
         print(build(verbose="-v" in sys.argv))

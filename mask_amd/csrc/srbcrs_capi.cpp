@@ -1219,7 +1219,7 @@ int srbcrs_plan_tune(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
     for (int32_t order : {SRBCRS_GRID_CHUNK_MAJOR, SRBCRS_GRID_CHUNK_SWEEP})
       for (int32_t wg : {128, 64, 256})
         for (int32_t depth : {2, 4}) {
-          if (wg == 256 && plan->blk_h != 32) continue;   // 32x32 only: two 128-column waves
+          // 256: for 32x32 two 128-column waves, for 16x8 one 256-column wave
           srbcrs_run_opts o{};
           o.depth = depth;
           o.wg_cols = wg;

@@ -122,7 +122,11 @@ struct DenseA {
 #pragma unroll
       for (int qq = 1; qq < S::Q; ++qq)
         if (q == qq) off = a_off[qq][h];
+#ifdef SRBCRS_EXPERIMENT_NO_A
+      a[h] = f2{1.f, (float)off};
+#else
       a[h] = *reinterpret_cast<const f2*>(vb + off);
+#endif
     }
   }
 };
@@ -179,8 +183,13 @@ __device__ __forceinline__ void load_frag(Frag<BH / 16, VEC, G>& f, const float*
   const float* r1 = B + (int64_t)rows.y * ldb + col0;
 #pragma unroll
   for (int g = 0; g < G; ++g) {
+#ifdef SRBCRS_EXPERIMENT_NO_B
+    f.b0[g] = V{} + (float)rows.x;
+    f.b1[g] = V{} + (float)rows.y;
+#else
     f.b0[g] = *reinterpret_cast<const V*>(r0 + 16 * VEC * g);
     f.b1[g] = *reinterpret_cast<const V*>(r1 + 16 * VEC * g);
+#endif
   }
 }
 
@@ -315,8 +324,12 @@ __device__ __forceinline__ void mma_frag(const Frag<H, VEC, G>& f, f4 (&acc)[H][
     for (int g = 0; g < G; ++g)
 #pragma unroll
       for (int s = 0; s < VEC; ++s) {
+#ifdef SRBCRS_EXPERIMENT_NO_MFMA
+        acc[h][g][s].x += f.a[h].x * vget<VEC>(f.b0[g], s) + f.a[h].y * vget<VEC>(f.b1[g], s);
+#else
         acc[h][g][s] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[h].x, vget<VEC>(f.b0[g], s), acc[h][g][s], 0, 0, 0);
         acc[h][g][s] = __builtin_amdgcn_mfma_f32_16x16x4f32(f.a[h].y, vget<VEC>(f.b1[g], s), acc[h][g][s], 0, 0, 0);
+#endif
       }
 }
 
@@ -345,7 +358,11 @@ __device__ __forceinline__ void store_tile(const f4 (&acc)[G][VEC], float* __res
 #pragma unroll
           for (int s = 0; s < VEC; ++s) v[s] = acc[g][s][r];
         }
+#ifdef SRBCRS_EXPERIMENT_PLAIN_C_STORE
+        *reinterpret_cast<V*>(p + 16 * VEC * g) = v;
+#else
         __builtin_nontemporal_store(v, reinterpret_cast<V*>(p + 16 * VEC * g));
+#endif
       }
     }
   }

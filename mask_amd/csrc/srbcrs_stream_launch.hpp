@@ -67,6 +67,8 @@ static hipError_t launch_d(const Src& src, const AF& af, int n_groups, const Str
   if (vec == 4 && o.b_lds)
     return (a.N % 128 == 0 && o.wg_cols != 64) ? launch_vg<AF, Src, 16, 8, 4, 2, DEPTH, 1>(src, af, n_groups, a, o, st)
                                               : launch_vg<AF, Src, 16, 8, 4, 1, DEPTH, 1>(src, af, n_groups, a, o, st);
+  if (vec == 4 && a.N % 256 == 0 && o.wg_cols >= 256)   // 256-column waves (G = 4)
+    return launch_vg<AF, Src, 16, 8, 4, 4, DEPTH>(src, af, n_groups, a, o, st);
   if (vec == 4)
     return (a.N % 128 == 0 && o.wg_cols != 64) ? launch_vg<AF, Src, 16, 8, 4, 2, DEPTH>(src, af, n_groups, a, o, st)
                                               : launch_vg<AF, Src, 16, 8, 4, 1, DEPTH>(src, af, n_groups, a, o, st);
