@@ -131,25 +131,26 @@ def build_sanitized() -> Path:
 # out, for timing only (their results are wrong on purpose and nothing but a
 # measurement loads them, through MASK_AMD_SRBCRS_LIB).
 EXPERIMENTS = {
-    "no_a": "SRBCRS_EXPERIMENT_NO_A",                  # dense A fragments not loaded
+    "no_a": "SRBCRS_EXPERIMENT_NO_A",                  # A fragments (dense or compact) not loaded
     "no_b": "SRBCRS_EXPERIMENT_NO_B",                  # B rows not gathered
     "no_mfma": "SRBCRS_EXPERIMENT_NO_MFMA",            # one VALU FMA per MFMA instead
     "plain_c_store": "SRBCRS_EXPERIMENT_PLAIN_C_STORE",  # C written with plain (not nontemporal) stores
+    "gather_only": "SRBCRS_EXPERIMENT_NO_A SRBCRS_EXPERIMENT_NO_MFMA",   # B gathers and C stores only
 }
 
 
 def build_experiment(name: str) -> Path:
-    """mask_amd/experiments/libmask_srbcrs_<name>.so with the macro of
+    """mask_amd/experiments/libmask_srbcrs_<name>.so with the macros of
     EXPERIMENTS[name] defined (objects under mask_amd/_build)."""
     from concurrent.futures import ThreadPoolExecutor
-    macro = EXPERIMENTS[name]
+    macros = [f"-D{m}=1" for m in EXPERIMENTS[name].split()]
     hipcc = _hipcc()
     out_dir = PKG / "_build" / "experiments" / name
     out_dir.mkdir(parents=True, exist_ok=True)
 
     def compile_obj(src):
         obj = out_dir / (src.rsplit(".", 1)[0] + ".o")
-        _run([hipcc, *DEVICE_FLAGS, f"-D{macro}=1", f"-I{ROOT / 'include'}", "-x", "hip", "-c", str(CSRC / src),
+        _run([hipcc, *DEVICE_FLAGS, *macros, f"-I{ROOT / 'include'}", "-x", "hip", "-c", str(CSRC / src),
               "-o", str(obj)])
         return str(obj)
 

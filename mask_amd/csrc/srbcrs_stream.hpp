@@ -147,7 +147,13 @@ struct CompactA {
     const int q = (int)(unit % S::Q);
     Meta<S::H> m;
 #pragma unroll
-    for (int h = 0; h < S::H; ++h) m.w[h] = words[blk * (S::SIZE / 32) + (pos<BW>(h, q, lane) >> 5)];
+    for (int h = 0; h < S::H; ++h) {
+#ifdef SRBCRS_EXPERIMENT_NO_A
+      m.w[h] = uint2{(uint32_t)blk, (uint32_t)q};
+#else
+      m.w[h] = words[blk * (S::SIZE / 32) + (pos<BW>(h, q, lane) >> 5)];
+#endif
+    }
     return m;
   }
   template <int BH, int BW>
@@ -162,8 +168,13 @@ struct CompactA {
       const uint32_t n = m.w[h].y + (uint32_t)__builtin_popcount(mask & ((1u << bit) - 1u));
       const uint32_t b0 = (mask >> bit) & 1u, b1 = (mask >> (bit + 1)) & 1u;
       float v0 = 0.f, v1 = 0.f;
+#ifdef SRBCRS_EXPERIMENT_NO_A
+      v0 = (float)n;
+      v1 = (float)(b0 + b1);
+#else
       if (b0) v0 = packed[n];
       if (b1) v1 = packed[n + b0];
+#endif
       a[h] = f2{v0, v1};
     }
   }
