@@ -136,6 +136,8 @@ EXPERIMENTS = {
     "no_mfma": "SRBCRS_EXPERIMENT_NO_MFMA",            # one VALU FMA per MFMA instead
     "plain_c_store": "SRBCRS_EXPERIMENT_PLAIN_C_STORE",  # C written with plain (not nontemporal) stores
     "gather_only": "SRBCRS_EXPERIMENT_NO_A SRBCRS_EXPERIMENT_NO_MFMA",   # B gathers and C stores only
+    "b_hit_quarter": "SRBCRS_EXPERIMENT_B_HIT_MASK=3",  # every 4th unit gathers B row 0 (a cache hit)
+    "b_hit_half": "SRBCRS_EXPERIMENT_B_HIT_MASK=1",     # every 2nd unit gathers B row 0
 }
 
 
@@ -143,7 +145,7 @@ def build_experiment(name: str) -> Path:
     """mask_amd/experiments/libmask_srbcrs_<name>.so with the macros of
     EXPERIMENTS[name] defined (objects under mask_amd/_build)."""
     from concurrent.futures import ThreadPoolExecutor
-    macros = [f"-D{m}=1" for m in EXPERIMENTS[name].split()]
+    macros = [f"-D{m}" if "=" in m else f"-D{m}=1" for m in EXPERIMENTS[name].split()]
     hipcc = _hipcc()
     out_dir = PKG / "_build" / "experiments" / name
     out_dir.mkdir(parents=True, exist_ok=True)

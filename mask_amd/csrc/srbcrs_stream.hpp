@@ -190,6 +190,9 @@ __device__ __forceinline__ void load_frag(Frag<BH / 16, VEC, G>& f, const float*
                                           int col0, int lane) {
   typedef typename VecT<VEC>::type V;
   asrc.template load<BH, BW>(f.a, unit, am, a_off, lane);
+#ifdef SRBCRS_EXPERIMENT_B_HIT_MASK
+  if ((unit & SRBCRS_EXPERIMENT_B_HIT_MASK) == SRBCRS_EXPERIMENT_B_HIT_MASK) rows = int2{0, 0};
+#endif
   const float* r0 = B + (int64_t)rows.x * ldb + col0;
   const float* r1 = B + (int64_t)rows.y * ldb + col0;
 #pragma unroll
