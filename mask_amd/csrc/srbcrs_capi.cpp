@@ -1230,16 +1230,17 @@ int srbcrs_plan_tune(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
     if (plan->sched.policy == "row")
       // several consecutive windows per wave: fewer waves than resident
       // slots, all sweeping their windows' columns in step
-      for (int32_t wpw : {4, 8})
-        for (int32_t depth : {2, 4, 8}) {
-          srbcrs_run_opts o{};
-          o.depth = depth;
-          o.wg_cols = 128;
-          o.grid_order = SRBCRS_GRID_CHUNK_MAJOR;
-          o.windows_per_wave = wpw;
-          o.a_operand = a;
-          cand.push_back(o);
-        }
+      for (int32_t wg : {128, 256})
+        for (int32_t wpw : {4, 8})
+          for (int32_t depth : {2, 4, 8}) {
+            srbcrs_run_opts o{};
+            o.depth = depth;
+            o.wg_cols = wg;
+            o.grid_order = SRBCRS_GRID_CHUNK_MAJOR;
+            o.windows_per_wave = wpw;
+            o.a_operand = a;
+            cand.push_back(o);
+          }
   }
   hipEvent_t e0 = nullptr, e1 = nullptr;
   int rc = guarded([&] {
