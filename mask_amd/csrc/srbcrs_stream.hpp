@@ -347,6 +347,20 @@ __device__ __forceinline__ void mma_frag(const Frag<H, VEC, G>& f, f4 (&acc)[H][
       }
 }
 
+// An int at p[i] for a wave-uniform i, read through the constant address
+// space so that the compiler emits a scalar load (counted on lgkmcnt).  Task
+// metadata is read this way: as a vector load it would be counted on vmcnt
+// with the B ring, and the wait for it at a task boundary would drain every
+// B load in flight.
+__device__ __forceinline__ int uniform_load(const int* __restrict__ p, int64_t i) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  typedef const __attribute__((address_space(4))) int cint;
+  return ((cint*)p)[i];
+#else
+  return p[i];
+#endif
+}
+
 // Store a 16 x (16*VEC*G) accumulator tile.  row0 is the tile's first
 // (packed) row, rows >= row_limit are skipped (M % 16 != 0).  With a row map
 // packed row p is written to output row rowmap[p] (reordered or sparse-row
@@ -357,11 +371,31 @@ __device__ __forceinline__ void store_tile(const f4 (&acc)[G][VEC], float* __res
                                            int lane, const int* __restrict__ rowmap = nullptr) {
   typedef typename VecT<VEC>::type V;
   const int k = lane >> 4;
+  // The tile's 16 map entries are read with scalar loads (clamped to the
+  // last row, so a partial tile stays in bounds) and each lane picks its
+  // four: a per-lane vector load here would be counted on vmcnt with the
+  // B ring, and its wait would drain every B load in flight at each flush.
+  // (int4 members, not an array: selects between array elements become
+  // indexed scratch loads)
+  int4 m0{}, m1{}, m2{}, m3{};
+  if (rowmap) {
+    auto at = [&](int i) { return uniform_load(rowmap, row0 + i < row_limit ? row0 + i : row_limit - 1); };
+    m0 = int4{at(0), at(1), at(2), at(3)};
+    m1 = int4{at(4), at(5), at(6), at(7)};
+    m2 = int4{at(8), at(9), at(10), at(11)};
+    m3 = int4{at(12), at(13), at(14), at(15)};
+  }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int64_t row = row0 + 4 * k + r;
     if (row < row_limit) {
-      const int64_t orow = rowmap ? (int64_t)rowmap[row] : row;
+      int64_t orow = row;
+      if (rowmap) {
+        auto c = [r](const int4& v) { return r == 0 ? v.x : r == 1 ? v.y : r == 2 ? v.z : v.w; };
+        const int lo = (k & 1) ? c(m1) : c(m0);
+        const int hi = (k & 1) ? c(m3) : c(m2);
+        orow = (k & 2) ? hi : lo;
+      }
       float* p = out + orow * ldc + col0;
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -386,20 +420,6 @@ __device__ __forceinline__ void store_tile(const f4 (&acc)[G][VEC], float* __res
 // whose BH-row result goes straight into C (slot < 0) or into partial slot
 // `slot` for the segment reduction.  A group is a run of consecutive tasks
 // with contiguous block ranges, processed by one wave per column chunk.
-
-// An int at p[i] for a wave-uniform i, read through the constant address
-// space so that the compiler emits a scalar load (counted on lgkmcnt).  Task
-// metadata is read this way: as a vector load it would be counted on vmcnt
-// with the B ring, and the wait for it at a task boundary would drain every
-// B load in flight.
-__device__ __forceinline__ int uniform_load(const int* __restrict__ p, int64_t i) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  typedef const __attribute__((address_space(4))) int cint;
-  return ((cint*)p)[i];
-#else
-  return p[i];
-#endif
-}
 
 // Row schedule: task t = row window t, groups of `wpw` consecutive windows.
 struct RowTasks {
