@@ -312,9 +312,10 @@ int srbcrs_stream_probe(int32_t kind, const float *d_a, float *d_b, int64_t n_fl
  * blocks, when the plan has the copy and at most 3/4 of the block positions
  * hold values), then for the dense one (unless, for 16x8, under 1/4 hold
  * values and the compact copy exists): grid order chunk-major /
- * chunk sweep x wg_cols 128 / 64 / 256 x depth 2 / 4, then, on the "row"
- * schedule, wg_cols 128 / 256 x 4 / 8 windows per wave x depth 2 / 4 / 8
- * (chunk-major).  Each gets one warm-up
+ * chunk sweep x wg_cols 128 / 64 / 256 x depth 2 / 4, then (16x8) the
+ * LDS-staged B ring at wg_cols 64, chunk sweep, depth 2 / 4, then, on the
+ * "row" schedule, wg_cols 128 / 256 x 4 / 8 windows per wave x depth
+ * 2 / 4 / 8 (chunk-major).  Each gets one warm-up
  * and `reps` timed launches on `stream`; the first candidate within 3 % of
  * the fastest wins, so near-ties resolve the same way on every run.  Later
  * srbcrs_run calls, and srbcrs_run_ex calls whose knobs are all 0, use it

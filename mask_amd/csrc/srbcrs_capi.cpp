@@ -1227,6 +1227,19 @@ int srbcrs_plan_tune(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
           o.a_operand = a;
           cand.push_back(o);
         }
+    if (!wide)
+      // B staged through LDS by direct-to-LDS loads, 64-column waves in the
+      // chunk sweep: its registers stay few enough for 5 waves per SIMD
+      // (measured 2-4 % ahead of the register ring on the skewed graphs)
+      for (int32_t depth : {2, 4}) {
+        srbcrs_run_opts o{};
+        o.depth = depth;
+        o.wg_cols = 64;
+        o.grid_order = SRBCRS_GRID_CHUNK_SWEEP;
+        o.a_operand = a;
+        o.b_stage = SRBCRS_B_LDS;
+        cand.push_back(o);
+      }
     if (plan->sched.policy == "row")
       // several consecutive windows per wave: fewer waves than resident
       // slots, all sweeping their windows' columns in step

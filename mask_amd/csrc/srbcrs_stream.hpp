@@ -541,9 +541,13 @@ __global__ __launch_bounds__(64 * WAVES) void spmm_stream(
     const int64_t last = ue - 1;
     if constexpr (BSTAGE == 1) {
       static_assert(VEC == 4, "LDS staging reads 16-byte B vectors");
+      static_assert(DEPTH % 2 == 0, "the B register pair alternates with the ring position");
       typedef LdsB<WCOLS> L;
       __shared__ __attribute__((aligned(16))) float lds_ring[WAVES * DEPTH * L::SLOT];
       float* my_ring = lds_ring + wave * DEPTH * L::SLOT;
+      // B of the unit being multiplied and of the next one, in registers:
+      // the next unit's LDS reads run under the current unit's MFMAs.
+      Frag<S::H, VEC, G> fb[2];
 #pragma unroll
       for (int d = 0; d < DEPTH; ++d) {
         const int64_t u = us + d < last ? us + d : last;
@@ -555,31 +559,66 @@ __global__ __launch_bounds__(64 * WAVES) void spmm_stream(
         idx[d].load(sidx, nu);
         am[d] = asrc.template meta<BH, BW>(nu, lane);
       }
-      for (int64_t base = us; base < ue; base += DEPTH) {
+      wait_vmcnt<(DEPTH - 1) * L::IPU>();   // slot 0 has landed
+      __builtin_amdgcn_sched_barrier(0);
+      L::template read<S::H, G>(fb[0], my_ring, lane);
+      // Steady state: unit u = base + d sits in slot d.  Its B was read into
+      // fb[d & 1] one step earlier; the wait below is for slot d + 1, with
+      // the DEPTH - 2 younger slots' B loads allowed in flight (every slot is
+      // refilled on every step, so that count is exact for the B loads; A
+      // loads in between only make the wait longer, never too short).
+      int64_t base = us;
+      for (; base + DEPTH < ue; base += DEPTH) {
 #pragma unroll
         for (int d = 0; d < DEPTH; ++d) {
           const int64_t u = base + d;
-          wait_vmcnt<(DEPTH - 1) * L::IPU>();
+          const int c = d & 1;
+          wait_lgkmcnt0();                    // fb[c] (and the scalar indices) ready
           __builtin_amdgcn_sched_barrier(0);
-          if (u < ue) {
-            while (u >= tend) {
-              flush_task<Src, BH, VEC, G>(src, t, acc, C, partial, M, ldc, col0, lane);
-              ++t;
-              tend = src.end(t) * S::Q;
-            }
-            L::template read<S::H, G>(f[d], my_ring + d * L::SLOT, lane);
-            mma_frag<S::H, VEC, G>(f[d], acc);
+          while (u >= tend) {
+            flush_task<Src, BH, VEC, G>(src, t, acc, C, partial, M, ldc, col0, lane);
+            ++t;
+            tend = src.end(t) * S::Q;
           }
-          wait_lgkmcnt0();
+#pragma unroll
+          for (int h = 0; h < S::H; ++h) fb[c].a[h] = f[d].a[h];
+          mma_frag<S::H, VEC, G>(fb[c], acc);
           __builtin_amdgcn_sched_barrier(0);
-          // refill the slot on every step (the last unit again past the end)
-          // so the count of younger loads in the wait above stays exact
+          wait_vmcnt<(DEPTH - 2) * L::IPU>();   // slot d + 1 has landed
+          __builtin_amdgcn_sched_barrier(0);
+          L::template read<S::H, G>(fb[c ^ 1], my_ring + ((d + 1) % DEPTH) * L::SLOT, lane);
+          __builtin_amdgcn_sched_barrier(0);
+          // refill slot d (its B was read into fb[c] a step ago)
           const int64_t nu = u + DEPTH < last ? u + DEPTH : last;
           asrc.template load<BH, BW>(f[d].a, nu, am[d], a_off, lane);
           L::issue(my_ring + d * L::SLOT, B, idx[d], ldb, wcol, lane);
-          const int64_t nn = u + 2 * DEPTH < last ? u + 2 * DEPTH : last;
+          const int64_t nn = nu + DEPTH < last ? nu + DEPTH : last;
           idx[d].load(sidx, nn);
           am[d] = asrc.template meta<BH, BW>(nn, lane);
+        }
+      }
+      // Drain: the last round's units are in the ring; nothing more to load.
+#pragma unroll
+      for (int d = 0; d < DEPTH; ++d) {
+        const int64_t u = base + d;
+        const int c = d & 1;
+        if (u < ue) {
+          wait_lgkmcnt0();
+          __builtin_amdgcn_sched_barrier(0);
+          while (u >= tend) {
+            flush_task<Src, BH, VEC, G>(src, t, acc, C, partial, M, ldc, col0, lane);
+            ++t;
+            tend = src.end(t) * S::Q;
+          }
+#pragma unroll
+          for (int h = 0; h < S::H; ++h) fb[c].a[h] = f[d].a[h];
+          mma_frag<S::H, VEC, G>(fb[c], acc);
+          __builtin_amdgcn_sched_barrier(0);
+          if (u + 1 < ue) {
+            wait_vmcnt<0>();
+            __builtin_amdgcn_sched_barrier(0);
+            L::template read<S::H, G>(fb[c ^ 1], my_ring + ((d + 1) % DEPTH) * L::SLOT, lane);
+          }
         }
       }
       wait_vmcnt<0>();
