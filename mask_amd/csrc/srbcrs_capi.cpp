@@ -1230,7 +1230,7 @@ int srbcrs_plan_tune(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
     if (!wide)
       // B staged through LDS by direct-to-LDS loads, 64-column waves in the
       // chunk sweep: its registers stay few enough for 5 waves per SIMD
-      // (measured 2-4 % ahead of the register ring on the skewed graphs)
+      // (measured 1.5-3 % ahead of the register ring on R-MAT)
       for (int32_t depth : {2, 4}) {
         srbcrs_run_opts o{};
         o.depth = depth;
