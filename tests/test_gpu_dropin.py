@@ -144,6 +144,13 @@ def test_packed_plans_match_oracle(gpu, packing, order, blk):
         plan.run(dB, out)
         torch.cuda.synchronize()
         assert_gate(gate(out.cpu().numpy(), rowptr, colind, values, B, M))   # duplicates summed
+    # the row map applied at task boundaries inside a wave's stream (several
+    # windows per wave), on both B rings: the same bits as one window per wave
+    plan.set_schedule("row", 0)
+    ref = plan.run(dB).cpu().numpy()
+    for wpw, stage, depth in ((3, "registers", 4), (3, "lds", 4), (16, "lds", 2), (16, "registers", 8)):
+        got = plan.run(dB, windows_per_wave=wpw, b_stage=stage, depth=depth).cpu().numpy()
+        assert np.array_equal(got, ref), (wpw, stage, depth)
 
 
 def test_generated_operator_on_packed_plan(gpu):
