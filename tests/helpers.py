@@ -68,3 +68,23 @@ def assert_gate(m, rel_l2=TOL_REL_L2):
     assert m["max_ratio"] <= TOL_ELEM, m
     assert m["rel_l2"] <= rel_l2, m
     assert m["ref_gate"], m
+
+
+# The reference harness's value protocol (custom_format_e2e.cu:1336-1342):
+# values p % 5 + 1 by CSR position, B element i = ((i % 29) - 14) / 14.
+def protocol_values(nnz: int) -> np.ndarray:
+    return (np.arange(nnz, dtype=np.int64) % 5 + 1).astype(np.float32)
+
+
+def protocol_dense(K: int, N: int) -> np.ndarray:
+    i = np.arange(K * N, dtype=np.int64)
+    return ((i % 29 - 14) / 14.0).astype(np.float32).reshape(K, N)
+
+
+def exact_product(rowptr, colind, values, B_int, M) -> np.ndarray:
+    """A @ B in int64 (duplicates collapsed to the last value first)."""
+    rp, ci, vv = dedupe_last(rowptr, colind, values)
+    out = np.zeros((M, B_int.shape[1]), np.int64)
+    rows = np.repeat(np.arange(M), np.diff(rp))
+    np.add.at(out, rows, vv.astype(np.int64)[:, None] * B_int.astype(np.int64)[ci])
+    return out

@@ -386,3 +386,21 @@ def test_segment_reduce_matches_numpy():
     exp = np.concatenate([partial[0] + partial[1], np.zeros((16, 8), np.float32),
                           partial[2] + partial[3] + partial[4]])
     assert np.array_equal(out, exp)
+
+
+def test_integer_protocol_product_matches_f64_oracle():
+    """The exact integer product the GPU protocol test compares against equals
+    the fp64 oracle's (fp64 is exact at these magnitudes), duplicates
+    included, and the protocol's dense values are what the reference writes."""
+    from tests.helpers import exact_product, protocol_dense, protocol_values, random_csr
+    assert protocol_values(7).tolist() == [1, 2, 3, 4, 5, 1, 2]
+    d = protocol_dense(2, 16)
+    assert d[0, 0] == np.float32(-1.0) and d[0, 14] == 0.0 and d[1, 0] == np.float32((16 % 29 - 14) / 14.0)
+    rowptr, colind, _ = random_csr(70, 90, 0.1, seed=5, unsorted=True, duplicates=True, empty_rows=0.1)
+    vals = protocol_values(colind.shape[0])
+    B = (14 * protocol_dense(90, 48)).round().astype(np.float32)
+    want = exact_product(rowptr, colind, vals, B, 70)
+    from tests.helpers import dedupe_last
+    rp, ci, vv = dedupe_last(rowptr, colind, vals)
+    C64 = oracle.csr_spmm_f64(rp, ci, vv, B, 70)
+    assert np.array_equal(np.asarray(C64), want.astype(np.float64))
