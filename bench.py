@@ -48,6 +48,9 @@ def parse():
     ap.add_argument("--kernel", default="srbcrs", choices=["srbcrs", "csr"])
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline leg")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--sustained-s", type=float, default=2.0,
+                    help="after the K timed steps, also time back-to-back steps for about this long "
+                         "(reported apart as 'sustained'; 0 = skip)")
     ap.add_argument("--no-check", action="store_true")
     ap.add_argument("--depth", type=int, default=0, help="kernel knob: blocks in flight per wave (2/4/8)")
     ap.add_argument("--tile-b", type=int, default=0, help="kernel knob: 16/32/64")
@@ -67,22 +70,31 @@ def parse():
                     help="kernel knob: where the ring holds the gathered B rows")
     ap.add_argument("--a-operand", default="default", choices=["default", "compact", "dense"],
                     help="block-value copy the kernel reads (default: compact when blocks are at most half full)")
+    ap.add_argument("--copy-seconds", type=float, default=0.0,
+                    help="with --copy-calibration-mb: repeat the copy for this long")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="only run an elementwise copy of this many MiB (5 launches) to calibrate "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE against a known byte count")
     return ap.parse_args()
 
 
-def copy_calibration(mib):
-    """Known-traffic reference kernel: out = in * 1 over mib MiB reads + writes."""
+def copy_calibration(mib, seconds=0.0):
+    """Known-traffic reference kernel: out = in * 1 over mib MiB reads + writes,
+    5 times, or back to back for `seconds` (a sustained copy load, the
+    reference point for system-level memory-controller activity)."""
     import torch
     n = mib * (1 << 20) // 4
     a = torch.ones(n, dtype=torch.float32, device="cuda")
     b = torch.empty_like(a)
-    for _ in range(5):
-        torch.mul(a, 1.0, out=b)
-    torch.cuda.synchronize()
-    print(json.dumps({"copy_calibration_bytes_read": n * 4, "copy_calibration_bytes_written": n * 4}))
+    reps, t0 = 0, time.time()
+    while reps < 5 or time.time() - t0 < seconds:
+        for _ in range(5 if seconds <= 0 else 50):
+            torch.mul(a, 1.0, out=b)
+            reps += 1
+        torch.cuda.synchronize()
+    el = time.time() - t0
+    print(json.dumps({"copy_calibration_bytes_read": n * 4, "copy_calibration_bytes_written": n * 4,
+                      "reps": reps, "gbs": round(2 * n * 4 * reps / el / 1e9, 1)}))
 
 
 def copy_bandwidth(mib=2048, reps=10):
@@ -364,7 +376,7 @@ def main():
         sys.exit(2)
 
     if args.copy_calibration_mb:
-        copy_calibration(args.copy_calibration_mb)
+        copy_calibration(args.copy_calibration_mb, args.copy_seconds)
         return
     if args.gcn_train:
         gcn_train_bench(args)
@@ -393,7 +405,7 @@ def main():
             if extra["roofline"].get("frac") is not None:
                 extra["roofline"]["frac_of_copy"] = round(extra["roofline"]["achieved"] / copy_gbs, 4)
             result["extra_configs"][name] = {k: extra[k] for k in (
-                "value", "unit", "ms_per_step", "ms_per_step_median", "config", "roofline", "parity",
+                "value", "unit", "ms_per_step", "ms_per_step_median", "config", "roofline", "sustained", "parity",
                 "cpu_baseline") if k in extra}
     print(json.dumps(result), flush=True)
 
@@ -495,6 +507,24 @@ def measure(args, config, mtx=None, cpu_seconds=None):
             and not mtx:
         prof = measured_profile(m.name, N, args.kernel, knobs, args.blk)
 
+    sustained = None
+    if args.sustained_s > 0:
+        # The clock settles only after the power management has reacted to
+        # the load (banded: boost, a dip, then a steady level), which a short
+        # K-step window can catch anywhere; this times the steady rate apart.
+        n_s = int(min(100000, max(args.steps, np.ceil(args.sustained_s * 1e3 / max(ms_step, 1e-3)))))
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(n_s):
+            step()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        ms_s = e0.elapsed_time(e1) / n_s
+        rs = roofline(ms_s / 1e3, ab, compulsory, padded_flops, prof)
+        sustained = {"steps": n_s, "seconds": round(ms_s * n_s / 1e3, 3), "ms_per_step": round(ms_s, 5),
+                     "value": round(flops / (ms_s / 1e3) / 1e9, 2), "frac": rs["frac"],
+                     "compulsory_frac": rs["compulsory_frac"]}
+
     result = {
         "metric": "SpMM GFLOP/s at N=512 fp32 on 1 MI355X; % of HBM roofline",
         "value": round(gflops, 2),
@@ -518,6 +548,8 @@ def measure(args, config, mtx=None, cpu_seconds=None):
         "roofline": roofline(t_s, ab, compulsory, padded_flops, prof),
         "wall_s_timed": round(wall, 4),
     }
+    if sustained is not None:
+        result["sustained"] = sustained
 
     budget = args.cpu_seconds if cpu_seconds is None else cpu_seconds
     if not (args.no_check and args.no_cpu):
