@@ -60,11 +60,9 @@ def build(verbose: bool = False) -> Path:
             print(out)
         return str(obj)
 
-    with ThreadPoolExecutor(max_workers=6) as ex:
+    with ThreadPoolExecutor(max_workers=8) as ex:
         gen = [ex.submit(build_generated_one, bm, bk, lds) for bm, bk, lds in GENERATED_SHAPES]
-        objs = list(ex.map(compile_obj, ("srbcrs_stream_compact.hip", "srbcrs_stream_dense.hip", "srbcrs_kernels.hip",
-                                         "srbcrs_capi.cpp", "srbcrs_pack.cpp", "srbcrs_convert.hip",
-                                         "srbcrs_compact.hip")))
+        objs = list(ex.map(compile_obj, SOURCES))
         for f in gen:
             f.result()
     tmp = LIB.with_suffix(".so.tmp")
@@ -73,6 +71,10 @@ def build(verbose: bool = False) -> Path:
     return LIB
 
 
+# translation units of the library, the slowest (the spmm_stream instantiations) first
+SOURCES = ("srbcrs_stream_compact.hip", "srbcrs_stream_compact_tasks.hip", "srbcrs_stream_dense.hip",
+           "srbcrs_stream_dense_tasks.hip", "srbcrs_kernels.hip", "srbcrs_capi.cpp", "srbcrs_pack.cpp",
+           "srbcrs_convert.hip", "srbcrs_compact.hip")
 GENERATED = PKG / "generated"
 # (block rows, block columns, B materialized in shared memory / LDS)
 GENERATED_SHAPES = ((16, 8, False), (32, 32, False), (16, 8, True))
@@ -118,10 +120,8 @@ def build_sanitized() -> Path:
               "-o", str(obj)])
         return str(obj)
 
-    with ThreadPoolExecutor(max_workers=6) as ex:
-        objs = list(ex.map(compile_obj, ("srbcrs_stream_compact.hip", "srbcrs_stream_dense.hip", "srbcrs_kernels.hip",
-                                         "srbcrs_capi.cpp", "srbcrs_pack.cpp", "srbcrs_convert.hip",
-                                         "srbcrs_compact.hip")))
+    with ThreadPoolExecutor(max_workers=8) as ex:
+        objs = list(ex.map(compile_obj, SOURCES))
     _run([hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-shared-libasan", "-fsanitize=address,undefined",
           "-o", str(SANITIZE_LIB), *objs, "-lpthread"])
     return SANITIZE_LIB
@@ -156,10 +156,8 @@ def build_experiment(name: str) -> Path:
               "-o", str(obj)])
         return str(obj)
 
-    with ThreadPoolExecutor(max_workers=6) as ex:
-        objs = list(ex.map(compile_obj, ("srbcrs_stream_compact.hip", "srbcrs_stream_dense.hip", "srbcrs_kernels.hip",
-                                         "srbcrs_capi.cpp", "srbcrs_pack.cpp", "srbcrs_convert.hip",
-                                         "srbcrs_compact.hip")))
+    with ThreadPoolExecutor(max_workers=8) as ex:
+        objs = list(ex.map(compile_obj, SOURCES))
     lib_dir = PKG / "experiments"
     lib_dir.mkdir(exist_ok=True)
     lib = lib_dir / f"libmask_srbcrs_{name}.so"

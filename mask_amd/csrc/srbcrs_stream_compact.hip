@@ -1,4 +1,4 @@
-// spmm_stream instantiations reading A through CompactA.
+// spmm_stream instantiations reading A through CompactA, row-window schedule.
 #include "srbcrs_stream_launch.hpp"
 
 namespace srbcrs {
@@ -6,11 +6,6 @@ namespace srbcrs {
 hipError_t launch_row_compact(const StreamArgs& a, const int* soff, int Mo, int vec, const RunOpts& o,
                       hipStream_t st) {
   return launch_row_af(CompactA{a.a_words, a.a_packed}, a, soff, Mo, vec, o, st);
-}
-
-hipError_t launch_tasks_compact(const StreamArgs& a, const TaskTable& t, int vec, const RunOpts& o,
-                        hipStream_t st) {
-  return launch_tasks_af(CompactA{a.a_words, a.a_packed}, a, t, vec, o, st);
 }
 
 }  // namespace srbcrs
