@@ -364,8 +364,9 @@ PUBLISHED_KNOBS = {
     # GCN aggregation at the workload's own width (N = 256), split schedule
     "gcn-232965": {"N": 256, "depth": 2, "wg_cols": 64, "grid_order": 3, "windows_per_wave": 1, "a_operand": "compact"},
 }
-# the second north-star configuration, measured in the same invocation as the headline
-EXTRA_CONFIGS = ("banded-524288",)
+# the other large configurations (banded: the second north-star target; R-MAT and the GCN
+# aggregation at N = 256), measured in the same invocation as the headline
+EXTRA_CONFIGS = ("banded-524288", "rmat-2^20", "gcn-232965")
 
 
 def main():
