@@ -164,3 +164,41 @@ def test_full_size_gcn_two_layer_forward(gpu):
         else:
             os.environ["SPARSENE_SRBCRS_VARIANT"] = old
         E.reset_backend_state()
+
+
+@pytest.mark.parametrize("name", ["uniform-65536", "banded-524288", "rmat-2^20", "gcn-232965"])
+def test_full_size_integer_protocol_exact(gpu, name):
+    """Every output element at full size, without a tolerance: the reference
+    harness's values p % 5 + 1 (custom_format_e2e.cu:1339) and a B of
+    integers -14..14 (14 x its ((i % 29) - 14) / 14, :1341) make every
+    partial sum an integer below 2^24, so fp32 is exact in any order and C
+    must equal the int64 product bit for bit, on every schedule the bench
+    uses (and the LDS ring)."""
+    import scipy.sparse as sp
+    import torch
+    from mask_amd.SRBCRSSpMM import Plan
+    from tests.helpers import protocol_dense, protocol_values
+    m = _workload(name)
+    N = 64
+    _say("full integer protocol", name, m.M, m.nnz, N)
+    vals = protocol_values(m.nnz)
+    B_int = (14 * protocol_dense(m.K, N)).round().astype(np.float32)
+    A = sp.csr_matrix((vals.astype(np.int64), m.colind, m.rowptr), shape=(m.M, m.K))
+    canon = A.copy()
+    canon.sum_duplicates()
+    assert canon.nnz == m.nnz              # no duplicate (row, col): last-write and sum agree
+    want = A @ B_int.astype(np.int64)
+    assert np.abs(want).max() < 2 ** 24
+    want = want.astype(np.float32)
+    dev = torch.device("cuda", 0)
+    t = lambda a: torch.from_numpy(a).to(dev)
+    plan = Plan(t(m.rowptr), t(m.colind), t(vals), m.M)
+    dB = t(B_int)
+    runs = [(("row", 0), {}), (("split", 0), {}), (("auto", 0), {})]
+    if name == "rmat-2^20":
+        runs.append((("split", 0), dict(depth=4, wg_cols=64, grid_order=3, b_stage="lds")))
+    for sched, knobs in runs:
+        _say("  schedule", sched, knobs)
+        plan.set_schedule(*sched)
+        C = plan.run(dB, **knobs).cpu().numpy()
+        assert np.array_equal(C, want), (name, sched, knobs, int((C != want).sum()))
