@@ -494,18 +494,28 @@ def measure(args, config, mtx=None, cpu_seconds=None, settle_s=0.0):
             warmup_done += 10
             torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
-    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
+    # The K timed steps run back to back between two events: a timing event
+    # recorded between two steps waits for the first to drain before the
+    # second starts, which would add a bubble per step to the timed region.
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_wall = time.perf_counter()
+    ev0.record(stream)
+    for i in range(args.steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_wall
+    total_ms = ev0.elapsed_time(ev1)
+    ms_step = total_ms / args.steps
+    # per-step times for the median: a separate pass of K steps, each between its own events
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps + 1)]
     evs[0].record(stream)
     for i in range(args.steps):
         step()
         evs[i + 1].record(stream)
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t_wall
     per = np.array([evs[i].elapsed_time(evs[i + 1]) for i in range(args.steps)])  # ms
-    total_ms = evs[0].elapsed_time(evs[-1])
-    ms_step = total_ms / args.steps
     t_s = ms_step / 1e3
     flops = 2.0 * m.nnz * N
     gflops = flops / t_s / 1e9
