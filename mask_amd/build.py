@@ -138,6 +138,7 @@ EXPERIMENTS = {
     "gather_only": "SRBCRS_EXPERIMENT_NO_A SRBCRS_EXPERIMENT_NO_MFMA",   # B gathers and C stores only
     "b_hit_quarter": "SRBCRS_EXPERIMENT_B_HIT_MASK=3",  # every 4th unit gathers B row 0 (a cache hit)
     "b_hit_half": "SRBCRS_EXPERIMENT_B_HIT_MASK=1",     # every 2nd unit gathers B row 0
+    "b_skip_two_thirds": "SRBCRS_EXPERIMENT_B_SKIP=3",  # only every 3rd unit gathers B (register ring)
 }
 
 

@@ -193,6 +193,11 @@ __device__ __forceinline__ void load_frag(Frag<BH / 16, VEC, G>& f, const float*
 #ifdef SRBCRS_EXPERIMENT_B_HIT_MASK
   if ((unit & SRBCRS_EXPERIMENT_B_HIT_MASK) == SRBCRS_EXPERIMENT_B_HIT_MASK) rows = int2{0, 0};
 #endif
+#ifdef SRBCRS_EXPERIMENT_B_SKIP
+  // the other units keep the previous B registers: as if neighbouring row
+  // windows shared those gathers
+  if (unit % SRBCRS_EXPERIMENT_B_SKIP != 0) return;
+#endif
   const float* r0 = B + (int64_t)rows.x * ldb + col0;
   const float* r1 = B + (int64_t)rows.y * ldb + col0;
 #pragma unroll
