@@ -511,6 +511,15 @@ __global__ __launch_bounds__(64 * WAVES) void spmm_stream(
   // are shared through the memory-side cache instead of each XCD holding a
   // different chunk.
   const int64_t lid = chunk_major == 2 ? (int64_t)blockIdx.x : xcd_remap(blockIdx.x, nwg);
+#ifdef SRBCRS_EXPERIMENT_LDS_PAD
+  if constexpr (BSTAGE == 0) {
+    // occupancy probe: unused LDS per workgroup caps the workgroups per CU
+    __shared__ float lds_pad[SRBCRS_EXPERIMENT_LDS_PAD / 4];
+    if (threadIdx.x == 0 && blockIdx.x == 0x7fffffff) lds_pad[0] = 0.f;
+    __syncthreads();
+    if (threadIdx.x == 0 && blockIdx.x == 0x7fffffff) C[0] = lds_pad[0];
+  }
+#endif
   const int64_t n_units = nwg / n_chunks;
   const int grp = (int)(chunk_major ? lid % n_units : lid / n_chunks);
   const int chunk = (int)(chunk_major ? lid / n_units : lid % n_chunks);
