@@ -72,6 +72,9 @@ def parse():
                     help="block-value copy the kernel reads (default: compact when blocks are at most half full)")
     ap.add_argument("--copy-seconds", type=float, default=0.0,
                     help="with --copy-calibration-mb: repeat the copy for this long")
+    ap.add_argument("--gather-study", action="store_true",
+                    help="only time the gather probe on the workload's own B-row index stream: unit order vs "
+                         "units of W windows merged by column, over grids and column-chunk widths")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="only run an elementwise copy of this many MiB (5 launches) to calibrate "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE against a known byte count")
@@ -97,6 +100,27 @@ def copy_calibration(mib, seconds=0.0):
                       "reps": reps, "gbs": round(2 * n * 4 * reps / el / 1e9, 1)}))
 
 
+# Measurement probes of the library (mask_amd/csrc/srbcrs_probe.h): internal,
+# not in the public C ABI, bound here only.
+PROBE_SIGS = {
+    "srbcrs_stream_probe": ("i32 vp vp i64 i32 vp"),
+    "srbcrs_gather_probe": ("vp vp i32 i32 vp i64 i32 i32 vp vp"),
+}
+
+
+def probes():
+    """The library with its probe entry points bound (ctypes)."""
+    import ctypes
+    from mask_amd import _capi
+    L = _capi.lib()
+    kinds = {"i32": ctypes.c_int32, "i64": ctypes.c_int64, "vp": ctypes.c_void_p}
+    for name, sig in PROBE_SIGS.items():
+        f = getattr(L, name)
+        f.argtypes = [kinds[k] for k in sig.split()]
+        f.restype = ctypes.c_int
+    return L
+
+
 def copy_bandwidth(mib=2048, reps=10):
     """What plain streaming kernels move on this box, as context for the
     SpMM's HBM-side rate: the library's float4 grid-stride probes
@@ -105,7 +129,7 @@ def copy_bandwidth(mib=2048, reps=10):
     sizes, best kept, HIP events on the launch stream.  GB/s of bytes moved."""
     import torch
     from mask_amd import _capi
-    L = _capi.lib()
+    L = probes()
     n = mib * (1 << 20) // 4
     a = torch.ones(n, dtype=torch.float32, device="cuda")
     b = torch.empty_like(a)
@@ -127,6 +151,104 @@ def copy_bandwidth(mib=2048, reps=10):
     del a, b
     torch.cuda.empty_cache()
     return out
+
+
+def gather_time(rows, row_off, rpi, B, ldb, n_chunks, mapping, reps=20):
+    """One srbcrs_gather_probe configuration, timed: (ms per launch, bytes
+    gathered per launch).  rows / row_off are host arrays (int32 / int64);
+    every row index is checked against B's rows before the upload."""
+    import torch
+    from mask_amd import _capi
+    L = probes()
+    n_rows_b = B.numel() // ldb
+    rows = np.ascontiguousarray(rows, dtype=np.int32)
+    row_off = np.ascontiguousarray(row_off, dtype=np.int64)
+    assert rows.size == 0 or (int(rows.min()) >= 0 and int(rows.max()) < n_rows_b), "row index outside B"
+    assert np.all(np.diff(row_off) % 8 == 0) and row_off[0] == 0 and row_off[-1] == rows.size
+    seg = 256 // rpi
+    assert n_chunks * seg <= ldb
+    n_groups = row_off.size - 1
+    d_rows = torch.from_numpy(rows).cuda()
+    d_off = torch.from_numpy(row_off).cuda()
+    nwg = (n_groups * n_chunks + 7) // 8 * 8
+    out = torch.empty(nwg * 64, device="cuda")
+    st = torch.cuda.current_stream().cuda_stream
+    call = lambda: _capi.check(L.srbcrs_gather_probe(d_rows.data_ptr(), d_off.data_ptr(), n_groups, rpi,
+                                                     B.data_ptr(), ldb, n_chunks, mapping, out.data_ptr(), st))
+    for _ in range(3):
+        call()
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(2)]
+    e[0].record()
+    for _ in range(reps):
+        call()
+    e[1].record()
+    torch.cuda.synchronize()
+    ms = e[0].elapsed_time(e[1]) / reps
+    return ms, int(rows.size) * n_chunks * seg * 4
+
+
+def gather_ceiling(n_lines=1 << 24, seed=7):
+    """What random gathers out of the L2 move on this box: n_lines uniformly
+    random 128-byte lines (eight per 1 KB load instruction) of a 134 MB
+    buffer, which the 256 MB memory-side cache holds, and of a 2.1 GB buffer,
+    which it does not; and the same bytes as random 1 KB row segments of the
+    134 MB buffer.  One XCD's 4 MB L2 holds 3 % of the smaller buffer, so
+    nearly every line leaves the L2: the rate is the L2-miss gather path's.
+    GB/s of gathered bytes (best of the XCD-blocked and dispatch-order grids)."""
+    import torch
+    rng = np.random.default_rng(seed)
+    out = {}
+    for name, mib, rpi in (("mall_128B", 128, 8), ("hbm_128B", 2048, 8), ("mall_1KB", 128, 1)):
+        seg = 256 // rpi
+        B = torch.ones(mib * (1 << 20) // 4, device="cuda")
+        n_rows_b = B.numel() // seg
+        n = n_lines * 128 // (seg * 4)
+        rows = rng.integers(0, n_rows_b, size=n, dtype=np.int64).astype(np.int32)
+        per = 2048 if rpi == 1 else 4096
+        row_off = np.arange(0, n + 1, per, dtype=np.int64)
+        best = 0.0
+        for mapping in (0, 1):
+            ms, nbytes = gather_time(rows, row_off, rpi, B, seg, 1, mapping)
+            best = max(best, nbytes / (ms / 1e3) / 1e9)
+        out[name] = round(best, 1)
+        del B
+        torch.cuda.empty_cache()
+    return out
+
+
+def gather_study(args):
+    """Gather-only timings (srbcrs_gather_probe) of the workload's own B-row
+    index stream at N = 512, printed as one JSON line: the kernel's unit order
+    (windows_per_wave W, 1 KB segments, the XCD-blocked chunk-major grid), and
+    the units of W windows merged by first column, with column chunks of 64,
+    128 or 256 columns pinned to XCDs (chunk = XCD % chunks)."""
+    import torch
+    from mask_amd import _capi, datasets
+    m = datasets.make_config(args.config)
+    conv = _capi.convert_host(m.rowptr, m.colind, m.values, m.M)
+    soff, sidx = conv["soff"].astype(np.int64), conv["sidx"].reshape(-1, 8)
+    N = 512
+    B = torch.from_numpy(m.dense(N)).cuda()
+    nb = sidx.shape[0]
+    win = np.repeat(np.arange(soff.size - 1), np.diff(soff))
+    res = []
+    for W, merge, rpi, mapping in ((8, False, 1, 1), (8, False, 4, 2), (8, True, 1, 2), (8, True, 2, 2),
+                                   (8, True, 4, 2), (4, True, 2, 2), (4, True, 4, 2), (16, True, 4, 2),
+                                   (32, True, 4, 2), (1, False, 4, 2), (1, False, 1, 1)):
+        grp = win // W
+        perm = np.lexsort((np.arange(nb), sidx[:, 0], grp)) if merge else np.arange(nb)
+        rows = sidx[perm].ravel()
+        row_off = np.zeros(grp.max() + 2, np.int64)
+        np.add.at(row_off, grp + 1, 8)
+        row_off = np.cumsum(row_off)
+        n_chunks = N // (256 // rpi)
+        ms, nbytes = gather_time(rows, row_off, rpi, B, N, n_chunks, mapping)
+        r = {"W": W, "merged": merge, "cols": 256 // rpi, "mapping": mapping, "ms": round(ms, 4),
+             "gbs": round(nbytes / ms / 1e6, 1)}
+        print("[gather-study]", r, file=sys.stderr, flush=True)
+        res.append(r)
+    print(json.dumps({"workload": m.name, "N": N, "gathered_bytes": int(nb * 8 * N * 4), "runs": res,
+                      "ceiling": gather_ceiling()}), flush=True)
 
 
 def gcn_forward_bench(args):
@@ -391,6 +513,9 @@ def main():
         return
     if args.gcn_forward:
         gcn_forward_bench(args)
+        return
+    if args.gather_study:
+        gather_study(args)
         return
 
     result = measure(args, args.config, mtx=args.mtx)

@@ -298,15 +298,6 @@ int srbcrs_run_noalloc(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N
                        void *stream);
 size_t srbcrs_noalloc_scratch_floats(void);
 
-/* Streaming-rate probe: one launch of a plain float4 grid-stride kernel
- * over n_floats floats (a multiple of 4, 16-byte aligned buffers) with
- * `blocks` workgroups of 256 threads: kind 0 copies d_a to d_b, 1 reads d_a
- * (d_b receives at most one float), 2 writes d_b.  No counterpart in the
- * reference: bench.py times it to report what plain streams move on the same
- * GPU next to the SpMM's HBM-side rate. */
-int srbcrs_stream_probe(int32_t kind, const float *d_a, float *d_b, int64_t n_floats, int32_t blocks,
-                        void *stream);
-
 /* Time candidate launch settings on this plan for a dense width N and keep
  * one.  Candidates, in preference order: for the compact A operand (16x8
  * blocks, when the plan has the copy and at most 3/4 of the block positions

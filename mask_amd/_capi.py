@@ -16,6 +16,11 @@ import os as _os
 # MASK_AMD_SRBCRS_LIB selects another build of the same library (the host
 # sanitizer build of mask_amd.build --sanitize); default: the in-tree one.
 LIB_PATH = Path(_os.environ.get("MASK_AMD_SRBCRS_LIB") or Path(__file__).resolve().parent / "libmask_srbcrs.so")
+# Decomposition builds (mask_amd.build --experiment) leave out part of the
+# SpMM's work on purpose and stamp srbcrs_version() with "+experiment:<name>".
+# The loader refuses such a library unless this variable is "1" (timing runs
+# of those builds only).
+ALLOW_EXPERIMENT_ENV = "MASK_AMD_ALLOW_EXPERIMENT"
 
 SRBCRS_OK = 0
 SRBCRS_EINVAL = -1
@@ -33,7 +38,6 @@ EXPORTS = (
     "srbcrs_plan_set_schedule", "srbcrs_run", "srbcrs_run_ex", "srbcrs_csr_spmm",
     "srbcrs_row_order", "srbcrs_pack_count", "srbcrs_pack_fill", "srbcrs_plan_create_ex", "srbcrs_plan_row_order",
     "srbcrs_plan_tune", "srbcrs_shard_windows", "srbcrs_run_noalloc", "srbcrs_noalloc_scratch_floats",
-    "srbcrs_stream_probe",
 )
 
 _i32p = ctypes.POINTER(ctypes.c_int32)
@@ -143,14 +147,23 @@ def lib() -> ctypes.CDLL:
         "srbcrs_run_noalloc": ([_vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64, ctypes.POINTER(RunOpts), _vp],
                                ctypes.c_int),
         "srbcrs_noalloc_scratch_floats": ([], ctypes.c_size_t),
-        "srbcrs_stream_probe": ([_i32, _vp, _vp, _i64, _i32, _vp], ctypes.c_int),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)
         f.argtypes = args
         f.restype = res
+    check_not_experiment(L.srbcrs_version().decode(), LIB_PATH)
     _lib = L
     return L
+
+
+def check_not_experiment(version: str, path) -> None:
+    """Refuse a decomposition build (results wrong on purpose) unless the
+    caller opted in through MASK_AMD_ALLOW_EXPERIMENT=1."""
+    if "+experiment:" in version and _os.environ.get(ALLOW_EXPERIMENT_ENV) != "1":
+        raise RuntimeError(
+            f"{path} is a decomposition build ({version}): its SpMM results are wrong on purpose. "
+            f"Set {ALLOW_EXPERIMENT_ENV}=1 only to time it.")
 
 
 def check(code: int) -> None:

@@ -74,7 +74,7 @@ def build(verbose: bool = False) -> Path:
 # translation units of the library, the slowest (the spmm_stream instantiations) first
 SOURCES = ("srbcrs_stream_compact.hip", "srbcrs_stream_compact_tasks.hip", "srbcrs_stream_dense.hip",
            "srbcrs_stream_dense_tasks.hip", "srbcrs_kernels.hip", "srbcrs_capi.cpp", "srbcrs_pack.cpp",
-           "srbcrs_convert.hip", "srbcrs_compact.hip")
+           "srbcrs_convert.hip", "srbcrs_compact.hip", "srbcrs_probe.hip")
 GENERATED = PKG / "generated"
 # (block rows, block columns, B materialized in shared memory / LDS)
 GENERATED_SHAPES = ((16, 8, False), (32, 32, False), (16, 8, True))
@@ -128,8 +128,10 @@ def build_sanitized() -> Path:
 
 
 # Decomposition builds: the same library with one part of the SpMM's work taken
-# out, for timing only (their results are wrong on purpose and nothing but a
-# measurement loads them, through MASK_AMD_SRBCRS_LIB).
+# out, for timing only.  Their results are wrong on purpose: srbcrs_version()
+# names the experiment and mask_amd._capi refuses to load such a build unless
+# MASK_AMD_ALLOW_EXPERIMENT=1 (set only by the timing runs that load it
+# through MASK_AMD_SRBCRS_LIB).
 EXPERIMENTS = {
     "no_a": "SRBCRS_EXPERIMENT_NO_A",                  # A fragments (dense or compact) not loaded
     "no_b": "SRBCRS_EXPERIMENT_NO_B",                  # B rows not gathered
@@ -148,6 +150,7 @@ def build_experiment(name: str) -> Path:
     EXPERIMENTS[name] defined (objects under mask_amd/_build)."""
     from concurrent.futures import ThreadPoolExecutor
     macros = [f"-D{m}" if "=" in m else f"-D{m}=1" for m in EXPERIMENTS[name].split()]
+    macros.append(f"-DSRBCRS_EXPERIMENT_TAG={name}")   # stamps srbcrs_version(); the loader refuses it
     hipcc = _hipcc()
     out_dir = PKG / "_build" / "experiments" / name
     out_dir.mkdir(parents=True, exist_ok=True)

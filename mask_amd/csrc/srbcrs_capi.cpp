@@ -20,6 +20,7 @@
 #include "srbcrs_kernels.h"
 #include "srbcrs_convert.h"
 #include "srbcrs_pack.h"
+#include "srbcrs_probe.h"
 
 namespace {
 
@@ -654,7 +655,15 @@ extern "C" {
 
 const char* srbcrs_last_error(void) { return g_last_error.c_str(); }
 
-const char* srbcrs_version(void) { return "mask_amd-srbcrs 0.1 gfx950"; }
+// A decomposition build (mask_amd/build.py --experiment) carries its name in
+// the version string, so that loaders can refuse it.
+#define SRBCRS_STR2(x) #x
+#define SRBCRS_STR(x) SRBCRS_STR2(x)
+#ifdef SRBCRS_EXPERIMENT_TAG
+const char* srbcrs_version(void) { return "mask_amd-srbcrs 0.2 gfx950+experiment:" SRBCRS_STR(SRBCRS_EXPERIMENT_TAG); }
+#else
+const char* srbcrs_version(void) { return "mask_amd-srbcrs 0.2 gfx950"; }
+#endif
 
 int srbcrs_convert_count(const int32_t* rowptr, const int32_t* colind, int32_t num_nodes,
                          int64_t nnz, int32_t blk_h, int32_t blk_w, int32_t* soff,
@@ -1196,6 +1205,25 @@ int srbcrs_stream_probe(int32_t kind, const float* d_a, float* d_b, int64_t n_fl
       fail(SRBCRS_EINVAL, "buffers must be 16-byte aligned");
     hip_check(srbcrs::launch_stream_probe(kind, d_a, d_b, n_floats / 4, blocks, static_cast<hipStream_t>(stream)),
               "launch stream probe");
+  });
+}
+
+int srbcrs_gather_probe(const int32_t* d_rows, const int64_t* d_row_off, int32_t n_groups, int32_t rows_per_instr,
+                        const float* d_B, int64_t ldb, int32_t n_chunks, int32_t mapping, float* d_out,
+                        void* stream) {
+  return guarded([&] {
+    if (rows_per_instr != 1 && rows_per_instr != 2 && rows_per_instr != 4 && rows_per_instr != 8)
+      fail(SRBCRS_EINVAL, "rows_per_instr must be 1, 2, 4 or 8");
+    if (n_groups < 0 || n_chunks < 1) fail(SRBCRS_EINVAL, "n_groups must be >= 0 and n_chunks >= 1");
+    if (mapping < 0 || mapping > 2) fail(SRBCRS_EINVAL, "mapping must be 0, 1 or 2");
+    if (mapping == 2 && 8 % n_chunks) fail(SRBCRS_EINVAL, "XCD-affine chunks need n_chunks to divide 8");
+    if (ldb < (int64_t)n_chunks * (256 / rows_per_instr) || ldb % 4)
+      fail(SRBCRS_EINVAL, "ldb must be a multiple of 4 covering n_chunks row segments");
+    if (!d_rows || !d_row_off || !d_B || !d_out) fail(SRBCRS_EINVAL, "buffer is NULL");
+    if (reinterpret_cast<uintptr_t>(d_B) % 16) fail(SRBCRS_EINVAL, "B must be 16-byte aligned");
+    hip_check(srbcrs::launch_gather_probe(d_rows, d_row_off, n_groups, rows_per_instr, d_B, ldb, n_chunks, mapping,
+                                          d_out, static_cast<hipStream_t>(stream)),
+              "launch gather probe");
   });
 }
 

@@ -79,7 +79,11 @@ hipError_t launch_tasks_compact(const StreamArgs& a, const TaskTable& t, int vec
 hipError_t launch_reduce(const ReduceArgs& a, int vec, hipStream_t st);
 hipError_t launch_csr(const CsrArgs& a, int vec, hipStream_t st);
 hipError_t launch_zero_rows(float* C, const int* rows, int n_rows, int N, int64_t ldc, hipStream_t st);
-// Streaming-rate probes (kind 0 copy a -> b, 1 read a, 2 write b), n4 float4 elements.
+// Measurement probes (srbcrs_probe.hip): streaming rates (kind 0 copy a -> b,
+// 1 read a, 2 write b, n4 float4 elements) and the gather probe.
 hipError_t launch_stream_probe(int kind, const float* a, float* b, int64_t n4, int blocks, hipStream_t st);
+hipError_t launch_gather_probe(const int* rows, const int64_t* row_off, int n_groups, int rows_per_instr,
+                               const float* B, int64_t ldb, int n_chunks, int mapping, float* out,
+                               hipStream_t st);
 
 }  // namespace srbcrs

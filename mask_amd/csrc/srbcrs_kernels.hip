@@ -67,39 +67,4 @@ hipError_t launch_zero_rows(float* C, const int* rows, int n_rows, int N, int64_
   return hipGetLastError();
 }
 
-// Streaming-rate probes: what plain float4 streams move on this GPU, the
-// context bench.py reports next to the SpMM's own HBM-side rate.  Grid-stride
-// loops (every thread ends after ceil(n4 / threads) iterations).
-namespace {
-typedef float pf4 __attribute__((ext_vector_type(4)));
-__global__ __launch_bounds__(256) void k_probe_copy(const pf4* __restrict__ a, pf4* __restrict__ b, int64_t n) {
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
-    __builtin_nontemporal_store(a[i], b + i);
-}
-__global__ __launch_bounds__(256) void k_probe_read(const pf4* __restrict__ a, float* __restrict__ sink, int64_t n) {
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  pf4 s = {0.f, 0.f, 0.f, 0.f};
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride) s += a[i];
-  // a data-dependent store the compiler cannot drop; taken only for a NaN sum
-  if (s.x + s.y + s.z + s.w != s.x + s.y + s.z + s.w) sink[0] = s.x;
-}
-__global__ __launch_bounds__(256) void k_probe_write(pf4* __restrict__ b, int64_t n) {
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  const pf4 v = {1.f, 2.f, 3.f, 4.f};
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += stride)
-    __builtin_nontemporal_store(v, b + i);
-}
-}  // namespace
-
-hipError_t launch_stream_probe(int kind, const float* a, float* b, int64_t n4, int blocks, hipStream_t st) {
-  if (n4 <= 0) return hipSuccess;
-  const auto* av = reinterpret_cast<const pf4*>(a);
-  auto* bv = reinterpret_cast<pf4*>(b);
-  if (kind == 0) hipLaunchKernelGGL(k_probe_copy, dim3(blocks), dim3(256), 0, st, av, bv, n4);
-  else if (kind == 1) hipLaunchKernelGGL(k_probe_read, dim3(blocks), dim3(256), 0, st, av, b, n4);
-  else hipLaunchKernelGGL(k_probe_write, dim3(blocks), dim3(256), 0, st, bv, n4);
-  return hipGetLastError();
-}
-
 }  // namespace srbcrs
