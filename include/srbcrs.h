@@ -203,14 +203,25 @@ int srbcrs_plan_set_schedule(srbcrs_plan *plan, const char *policy, int32_t para
  * Requirements: N % 16 == 0, K > max column, c_rows >=
  * num_nodes (rows beyond num_nodes are not written).  Every row
  * < num_nodes of C is overwritten (zeros for empty windows).  Schedules
- * other than "row" use a plan-owned partial buffer, grown (hipMalloc) when a
- * run needs more slots x ldc than it holds.  Growth never frees: replaced
- * buffers and replaced task tables stay allocated until
- * srbcrs_plan_destroy, so a HIP graph captured on an earlier run keeps
- * valid addresses.  Capture after one eager run with the same N, ldc and
- * schedule (a growing run allocates, which graph capture forbids). */
+ * other than "row" use a plan-owned partial buffer, grown (hipMalloc, to at
+ * least twice its size) when a run needs more slots x ldc than it holds.
+ * Growth never frees: replaced buffers and replaced task tables are retired
+ * and stay allocated until srbcrs_plan_trim or srbcrs_plan_destroy, so a HIP
+ * graph captured on an earlier run keeps valid addresses.  Capture after one
+ * eager run with the same N, ldc and schedule (a growing run allocates,
+ * which graph capture forbids).  A call that is refused (a negative status)
+ * has launched nothing and left C untouched. */
 int srbcrs_run(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int64_t ldb,
                float *d_C, int64_t ldc, int64_t c_rows, void *stream);
+
+/* Free the device buffers the plan has retired (partial buffers it grew
+ * out of, task tables of earlier schedules) after synchronizing `stream`.
+ * Retired buffers are what graphs captured on earlier runs may still
+ * address: call this only when no such graph will be replayed again and no
+ * launch that used them is in flight on another stream.  Without it they
+ * are freed with the plan.  No reference counterpart (the reference keeps
+ * one global cache entry). */
+int srbcrs_plan_trim(srbcrs_plan *plan, void *stream);
 
 /* Launch knobs of the SR-BCRS kernels (template parameters; each maps a
  * knob of the reference's strategy schema, strategy_agent.py:81-130):
@@ -232,7 +243,17 @@ int srbcrs_run(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int64_
  *                chunk of every window before the next chunk (narrower B
  *                working set per XCD), 2 = window-major, 3 = chunk sweep:
  *                chunk-major in dispatch order, all XCDs on one chunk at a
- *                time (its B rows shared through the memory-side cache);
+ *                time (its B rows shared through the memory-side cache),
+ *                4 = merged windows ("row" schedule, 16x8 blocks with the
+ *                compact A copy, vector width 4): one wave per
+ *                windows_per_wave windows (4 or 8; 0 = 8) and wg_cols
+ *                columns (64 or 128; 0 = 64), walking the
+ *                windows' blocks interleaved (block r of each window in
+ *                turn) so that it sweeps its B rows once in ascending order,
+ *                the column chunk pinned to one XCD (N / wg_cols must divide
+ *                8 or be a multiple of 8); depth 2 or 4.  The first run per
+ *                windows_per_wave builds the interleaved copy of the block
+ *                indices and A words on the host (it allocates);
  *   windows_per_wave  "row" schedule: consecutive row windows one wave
  *                streams through its register ring (0 = 1), in [0, 4096];
  *   a_operand    see SRBCRS_A_* below;
@@ -274,6 +295,7 @@ typedef struct srbcrs_run_opts {
 #define SRBCRS_GRID_CHUNK_MAJOR 1
 #define SRBCRS_GRID_WINDOW_MAJOR 2
 #define SRBCRS_GRID_CHUNK_SWEEP 3
+#define SRBCRS_GRID_MERGED 4
 
 /* srbcrs_run with explicit knobs (opts NULL = defaults). */
 int srbcrs_run_ex(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int64_t ldb,

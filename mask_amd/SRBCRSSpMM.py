@@ -147,7 +147,8 @@ class Plan:
             b_stage: str = "default") -> Tensor:
         """out[:num_nodes] = A @ dense on the current stream.  The keyword
         knobs are the kernel template parameters (srbcrs_run_opts; 0 =
-        default; grid_order 1 = chunk-major, 2 = window-major, 3 = chunk sweep; a_operand
+        default; grid_order 1 = chunk-major, 2 = window-major, 3 = chunk sweep, 4 = merged
+        windows ("row" schedule: windows_per_wave windows interleaved per wave); a_operand
         "compact" / "dense" picks the block-value copy the kernel reads; b_stage
         "registers" / "lds" where the ring holds the gathered B rows)."""
         out = self._operands(dense, out)
@@ -176,6 +177,13 @@ class Plan:
         return {"depth": best.depth, "wg_cols": best.wg_cols, "grid_order": best.grid_order,
                 "windows_per_wave": best.windows_per_wave or 1, "a_operand": inv[best.a_operand],
                 "b_stage": "lds" if best.b_stage == 2 else "registers"}
+
+    def trim(self) -> None:
+        """Free the device buffers the plan retired (srbcrs_plan_trim) after
+        synchronizing the current stream; only when no captured graph of an
+        earlier run will be replayed."""
+        with torch.cuda.device(self.device):
+            _capi.check(_capi.lib().srbcrs_plan_trim(self._h, _stream_handle(self.device)))
 
     def row_order(self):
         """The plan's row order (new -> original) as a numpy array."""

@@ -38,6 +38,7 @@ EXPORTS = (
     "srbcrs_plan_set_schedule", "srbcrs_run", "srbcrs_run_ex", "srbcrs_csr_spmm",
     "srbcrs_row_order", "srbcrs_pack_count", "srbcrs_pack_fill", "srbcrs_plan_create_ex", "srbcrs_plan_row_order",
     "srbcrs_plan_tune", "srbcrs_shard_windows", "srbcrs_run_noalloc", "srbcrs_noalloc_scratch_floats",
+    "srbcrs_plan_trim",
 )
 
 _i32p = ctypes.POINTER(ctypes.c_int32)
@@ -147,6 +148,7 @@ def lib() -> ctypes.CDLL:
         "srbcrs_run_noalloc": ([_vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64, ctypes.POINTER(RunOpts), _vp],
                                ctypes.c_int),
         "srbcrs_noalloc_scratch_floats": ([], ctypes.c_size_t),
+        "srbcrs_plan_trim": ([_vp, _vp], ctypes.c_int),
     }
     for name, (args, res) in sig.items():
         f = getattr(L, name)

@@ -72,7 +72,7 @@ def build(verbose: bool = False) -> Path:
 
 
 # translation units of the library, the slowest (the spmm_stream instantiations) first
-SOURCES = ("srbcrs_stream_compact.hip", "srbcrs_stream_compact_tasks.hip", "srbcrs_stream_dense.hip",
+SOURCES = ("srbcrs_merged.hip", "srbcrs_stream_compact.hip", "srbcrs_stream_compact_tasks.hip", "srbcrs_stream_dense.hip",
            "srbcrs_stream_dense_tasks.hip", "srbcrs_kernels.hip", "srbcrs_capi.cpp", "srbcrs_pack.cpp",
            "srbcrs_convert.hip", "srbcrs_compact.hip", "srbcrs_probe.hip")
 GENERATED = PKG / "generated"
@@ -138,6 +138,7 @@ EXPERIMENTS = {
     "no_mfma": "SRBCRS_EXPERIMENT_NO_MFMA",            # one VALU FMA per MFMA instead
     "plain_c_store": "SRBCRS_EXPERIMENT_PLAIN_C_STORE",  # C written with plain (not nontemporal) stores
     "gather_only": "SRBCRS_EXPERIMENT_NO_A SRBCRS_EXPERIMENT_NO_MFMA",   # B gathers and C stores only
+    "mfma_only": "SRBCRS_EXPERIMENT_NO_A SRBCRS_EXPERIMENT_NO_B",        # MFMAs, indices and C stores only
     "b_hit_quarter": "SRBCRS_EXPERIMENT_B_HIT_MASK=3",  # every 4th unit gathers B row 0 (a cache hit)
     "b_hit_half": "SRBCRS_EXPERIMENT_B_HIT_MASK=1",     # every 2nd unit gathers B row 0
     "b_skip_two_thirds": "SRBCRS_EXPERIMENT_B_SKIP=3",  # only every 3rd unit gathers B (register ring)

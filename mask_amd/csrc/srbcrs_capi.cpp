@@ -444,6 +444,15 @@ struct srbcrs_plan {
   // launch settings chosen by srbcrs_plan_tune, per dense width N, for the
   // current schedule (cleared when it changes)
   std::map<int64_t, srbcrs_run_opts> tuned;
+  // interleaved unit streams of the merged-window grid, per windows-per-group
+  // W (built on first use, kept until the plan is destroyed)
+  struct Merged {
+    int32_t* d_moff = nullptr;   // group g's units: [moff[g], moff[g+1])
+    int32_t* d_sidx = nullptr;   // 8 B-row indices per unit, -1 for null units
+    uint2* d_words = nullptr;    // compact A words per unit, zero for null units
+    int64_t units = 0;
+  };
+  std::map<int, Merged> merged;
 
   template <class T>
   void retire(T*& p) {
@@ -476,6 +485,11 @@ struct srbcrs_plan {
     dev_free(d_bp);
     dev_free(d_awords);
     dev_free(d_apacked);
+    for (auto& kv : merged) {
+      dev_free(kv.second.d_moff);
+      dev_free(kv.second.d_sidx);
+      dev_free(kv.second.d_words);
+    }
     if (switched) (void)hipSetDevice(cur);
   }
 };
@@ -647,6 +661,68 @@ void build_compact(srbcrs_plan& plan, hipStream_t st) {
   plan.d_awords = c.words;
   plan.d_apacked = c.packed;
   plan.n_apacked = c.n_packed;
+}
+
+// The interleaved unit stream of the merged-window grid for groups of W row
+// windows (spmm_merged, srbcrs_merged.hpp): group g = windows [gW, gW + W);
+// its stream is R rounds of W units, round r holding block r of each window
+// (null units where a window has fewer than R blocks, and for the slots past
+// the last window).  Built on the host from the plan's sidx and compact A
+// words (copied down once), uploaded once per W.
+const srbcrs_plan::Merged& merged_stream(srbcrs_plan& plan, int W, hipStream_t st) {
+  auto it = plan.merged.find(W);
+  if (it != plan.merged.end()) return it->second;
+  const int64_t nb = plan.total;
+  const int Mo = plan.Mo;
+  constexpr int kWords = 16 * 8 / 32;   // compact A words per 16x8 block
+  std::vector<int32_t> sidx((size_t)nb * 8);
+  std::vector<uint2> words((size_t)nb * kWords);
+  if (nb) {
+    hip_check(hipMemcpyAsync(sidx.data(), plan.d_sidx, sidx.size() * sizeof(int32_t), hipMemcpyDeviceToHost, st),
+              "hipMemcpyAsync sidx D2H");
+    hip_check(hipMemcpyAsync(words.data(), plan.d_awords, words.size() * sizeof(uint2), hipMemcpyDeviceToHost, st),
+              "hipMemcpyAsync A words D2H");
+    hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
+  }
+  const int64_t n_groups = (Mo + W - 1) / W;
+  std::vector<int32_t> moff((size_t)n_groups + 1, 0);
+  for (int64_t g = 0; g < n_groups; ++g) {
+    int32_t rounds = 0;
+    for (int w = (int)(g * W); w < Mo && w < (g + 1) * W; ++w)
+      rounds = std::max(rounds, plan.h_soff[w + 1] - plan.h_soff[w]);
+    const int64_t next = (int64_t)moff[g] + (int64_t)rounds * W;
+    if (next > INT32_MAX) fail(SRBCRS_EINVAL, "the merged-window stream exceeds 2^31 units");
+    moff[g + 1] = (int32_t)next;
+  }
+  const int64_t units = moff[n_groups];
+  std::vector<int32_t> msidx((size_t)units * 8, -1);
+  std::vector<uint2> mwords((size_t)units * kWords, uint2{0u, 0u});
+  parallel_for(n_groups, [&](int64_t lo, int64_t hi) {
+    for (int64_t g = lo; g < hi; ++g)
+      for (int w = 0; w < W; ++w) {
+        const int64_t win = g * W + w;
+        if (win >= Mo) break;
+        const int32_t b0 = plan.h_soff[win], b1 = plan.h_soff[win + 1];
+        for (int32_t b = b0; b < b1; ++b) {
+          const int64_t u = moff[g] + (int64_t)(b - b0) * W + w;
+          std::copy_n(&sidx[(size_t)b * 8], 8, &msidx[(size_t)u * 8]);
+          std::copy_n(&words[(size_t)b * kWords], kWords, &mwords[(size_t)u * kWords]);
+        }
+      }
+  });
+  srbcrs_plan::Merged m;
+  try {
+    m.d_moff = upload(moff);
+    m.d_sidx = upload(msidx);
+    m.d_words = upload(mwords);
+  } catch (...) {
+    dev_free(m.d_moff);
+    dev_free(m.d_sidx);
+    dev_free(m.d_words);
+    throw;
+  }
+  m.units = units;
+  return plan.merged.emplace(W, m).first->second;
 }
 
 }  // namespace
@@ -1049,8 +1125,8 @@ static void run_impl(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
         fail(SRBCRS_EINVAL, "tile_b must be 0, 16, 32 or 64 (got %d)", opts->tile_b);
       if (opts->wg_cols != 0 && (opts->wg_cols < 64 || opts->wg_cols > 512 || (opts->wg_cols & (opts->wg_cols - 1))))
         fail(SRBCRS_EINVAL, "wg_cols must be 0 or a power of two in [64, 512] (got %d)", opts->wg_cols);
-      if (opts->grid_order < 0 || opts->grid_order > 3)
-        fail(SRBCRS_EINVAL, "grid_order must be 0, 1, 2 or 3 (got %d)", opts->grid_order);
+      if (opts->grid_order < 0 || opts->grid_order > 4)
+        fail(SRBCRS_EINVAL, "grid_order must be 0, 1, 2, 3 or 4 (got %d)", opts->grid_order);
       if (opts->depth) ro.depth = opts->depth;
       if (opts->wg_cols) ro.wg_cols = opts->wg_cols;
       if (opts->grid_order)
@@ -1103,10 +1179,39 @@ static void run_impl(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
       vec /= 2;
     srbcrs::StreamArgs a{d_B, d_C, nullptr, plan->d_sidx, plan->d_val, (int)plan->packed_rows, (int)N, ldb, ldc,
                          plan->blk_h, plan->d_rowmap, plan->d_awords, plan->d_apacked};
-    if (plan->n_zero_rows)
-      hip_check(srbcrs::launch_zero_rows(d_C, plan->d_zero_rows, plan->n_zero_rows, (int)N, ldc, st),
-                "launch zero_rows");
+    // Everything that can refuse the call, and every allocation, comes before
+    // the first launch: a refused call leaves C untouched.
+    const bool merged = opts && opts->grid_order == SRBCRS_GRID_MERGED;
+    if (merged) {
+      const int cols = ro.wg_cols == 128 ? 128 : 64;
+      const int W = opts->windows_per_wave ? opts->windows_per_wave : 8;
+      if (plan->sched.policy != "row") fail(SRBCRS_EINVAL, "the merged-window grid runs the \"row\" schedule only");
+      if (plan->blk_h != 16 || (!plan->d_awords && plan->total > 0))
+        fail(SRBCRS_EINVAL, "the merged-window grid needs 16x8 blocks with the compact copy of the block values");
+      if (opts->a_operand == SRBCRS_A_DENSE || opts->b_stage == SRBCRS_B_LDS)
+        fail(SRBCRS_EINVAL, "the merged-window grid reads the compact A copy and keeps B in registers");
+      if (ro.wg_cols != 64 && ro.wg_cols != 128) fail(SRBCRS_EINVAL, "the merged-window grid takes wg_cols 64 or 128");
+      if (ro.depth != 2 && ro.depth != 4) fail(SRBCRS_EINVAL, "the merged-window grid takes depth 2 or 4");
+      if (W != 4 && W != 8) fail(SRBCRS_EINVAL, "the merged-window grid takes windows_per_wave 4 or 8");
+      if (vec != 4) fail(SRBCRS_EINVAL, "the merged-window grid needs N, ldb, ldc multiples of 64 / 4 / 4 and "
+                                        "16-byte aligned B and C");
+      if (!srbcrs::merged_chunks_ok((int)(N / cols)))
+        fail(SRBCRS_EINVAL, "the merged-window grid needs N / %d column chunks to divide 8 or be a multiple of 8", cols);
+      if (fixed_partial && !plan->merged.count(W))
+        fail(SRBCRS_EINVAL, "the merged-window stream for %d windows is not built yet: call srbcrs_run_ex once with "
+                            "these knobs first (it allocates)", W);
+      const srbcrs_plan::Merged& m = merged_stream(*plan, W, st);
+      if (plan->n_zero_rows)
+        hip_check(srbcrs::launch_zero_rows(d_C, plan->d_zero_rows, plan->n_zero_rows, (int)N, ldc, st),
+                  "launch zero_rows");
+      srbcrs::MergedArgs ma{m.d_moff, plan->Mo, W, m.d_sidx, m.d_words};
+      hip_check(srbcrs::launch_merged(ma, a, cols, ro.depth, st), "launch spmm_merged");
+      return;
+    }
     if (plan->sched.policy == "row") {
+      if (plan->n_zero_rows)
+        hip_check(srbcrs::launch_zero_rows(d_C, plan->d_zero_rows, plan->n_zero_rows, (int)N, ldc, st),
+                  "launch zero_rows");
       hip_check(srbcrs::launch_row(a, plan->d_soff, plan->Mo, vec, ro, st), "launch spmm_stream(row)");
       return;
     }
@@ -1121,16 +1226,22 @@ static void run_impl(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
              need, s.n_slots, plan->blk_h, (long long)ldc, fixed_cap);
     } else {
       if (need > plan->partial_cap) {
-        // grow-only; the old buffer is retired, not freed (launches in flight
-        // and captured graphs keep a valid address), so no stream sync here
-        float* grown = dev_alloc<float>(need);
+        // grow-only, geometrically (a plan whose N or ldc rises step by step
+        // reallocates O(log) times); the old buffer is retired, not freed
+        // (launches in flight and captured graphs keep a valid address), so
+        // no stream sync here.  srbcrs_plan_trim frees retired buffers.
+        const size_t cap = std::max(need, 2 * plan->partial_cap);
+        float* grown = dev_alloc<float>(cap);
         plan->retire(plan->d_partial);
         plan->d_partial = grown;
-        plan->partial_cap = need;
+        plan->partial_cap = cap;
       }
       partial = plan->d_partial;
     }
     a.partial = partial;
+    if (plan->n_zero_rows)
+      hip_check(srbcrs::launch_zero_rows(d_C, plan->d_zero_rows, plan->n_zero_rows, (int)N, ldc, st),
+                "launch zero_rows");
     srbcrs::TaskTable tt{plan->d_group_off, plan->d_task_begin, plan->d_task_end, plan->d_task_window,
                          plan->d_task_slot, (int)s.group_off.size() - 1};
     hip_check(srbcrs::launch_tasks(a, tt, vec, ro, st), "launch spmm_stream(tasks)");
@@ -1193,6 +1304,20 @@ int srbcrs_run_noalloc(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N
 }
 
 size_t srbcrs_noalloc_scratch_floats(void) { return kNoallocScratchFloats; }
+
+int srbcrs_plan_trim(srbcrs_plan* plan, void* stream) {
+  return guarded([&] {
+    if (!plan) fail(SRBCRS_EINVAL, "plan is NULL");
+    int cur = 0;
+    hip_check(hipGetDevice(&cur), "hipGetDevice");
+    if (cur != plan->device) fail(SRBCRS_ESTATE, "plan lives on device %d, current device is %d", plan->device, cur);
+    // every launch that could still read a retired buffer was queued on this
+    // stream (or on work the caller has already waited for)
+    hip_check(hipStreamSynchronize(static_cast<hipStream_t>(stream)), "hipStreamSynchronize");
+    for (void* p : plan->retired) (void)hipFree(p);
+    plan->retired.clear();
+  });
+}
 
 int srbcrs_stream_probe(int32_t kind, const float* d_a, float* d_b, int64_t n_floats, int32_t blocks,
                         void* stream) {

@@ -32,6 +32,17 @@ struct StreamArgs {
   const float* a_packed = nullptr;
 };
 
+// Merged-window operands (spmm_merged): the row schedule's windows in groups
+// of W; group g's unit stream is [moff[g], moff[g+1]) of the interleaved
+// copies of sidx (8 per unit, -1 for null units) and of the compact A words.
+struct MergedArgs {
+  const int* moff;
+  int Mo;
+  int W;
+  const int* sidx;
+  const uint2* words;
+};
+
 struct TaskTable {
   const int* group_off;
   const int* task_begin;
@@ -76,6 +87,10 @@ hipError_t launch_row_compact(const StreamArgs& a, const int* soff, int Mo, int 
                               hipStream_t st);
 hipError_t launch_tasks_compact(const StreamArgs& a, const TaskTable& t, int vec, const RunOpts& o,
                                 hipStream_t st);
+// spmm_merged: cols 64 (W 4 or 8) or 128 (W 4), depth 2 or 4, vector width 4,
+// a.N / cols column chunks, which merged_chunks_ok must accept.
+hipError_t launch_merged(const MergedArgs& m, const StreamArgs& a, int cols, int depth, hipStream_t st);
+bool merged_chunks_ok(int n_chunks);
 hipError_t launch_reduce(const ReduceArgs& a, int vec, hipStream_t st);
 hipError_t launch_csr(const CsrArgs& a, int vec, hipStream_t st);
 hipError_t launch_zero_rows(float* C, const int* rows, int n_rows, int N, int64_t ldc, hipStream_t st);
