@@ -251,7 +251,8 @@ int srbcrs_plan_trim(srbcrs_plan *plan, void *stream);
  *                windows' blocks interleaved (block r of each window in
  *                turn) so that it sweeps its B rows once in ascending order,
  *                the column chunk pinned to one XCD (N / wg_cols must divide
- *                8 or be a multiple of 8); depth 2 or 4.  The first run per
+ *                8 or be a multiple of 8); depth 2 or 4 (8 windows: only
+ *                at 64 columns and depth 2).  The first run per
  *                windows_per_wave builds the interleaved copy of the block
  *                indices and A words on the host (it allocates);
  *   windows_per_wave  "row" schedule: consecutive row windows one wave
@@ -328,7 +329,10 @@ size_t srbcrs_noalloc_scratch_floats(void);
  * chunk sweep x wg_cols 128 / 64 / 256 x depth 2 / 4, then (16x8) the
  * LDS-staged B ring at wg_cols 64, chunk sweep, depth 2 / 4, then, on the
  * "row" schedule, wg_cols 128 / 256 x 4 / 8 windows per wave x depth
- * 2 / 4 / 8 (chunk-major).  Each gets one warm-up
+ * 2 / 4 / 8 (chunk-major), and last, for the compact A source on the "row"
+ * schedule, the merged-window grid at (wg_cols, windows, depth) = (128, 4,
+ * 4), (128, 4, 2), (64, 8, 2), (64, 4, 4) where N allows it (a setting the
+ * operands' alignment refuses is skipped).  Each gets one warm-up
  * and `reps` timed launches on `stream`; the first candidate within 3 % of
  * the fastest wins, so near-ties resolve the same way on every run.  Later
  * srbcrs_run calls, and srbcrs_run_ex calls whose knobs are all 0, use it

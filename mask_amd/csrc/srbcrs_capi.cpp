@@ -3,6 +3,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <array>
 #include <atomic>
 #include <cmath>
 #include <cstdarg>
@@ -1193,6 +1194,8 @@ static void run_impl(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
       if (ro.wg_cols != 64 && ro.wg_cols != 128) fail(SRBCRS_EINVAL, "the merged-window grid takes wg_cols 64 or 128");
       if (ro.depth != 2 && ro.depth != 4) fail(SRBCRS_EINVAL, "the merged-window grid takes depth 2 or 4");
       if (W != 4 && W != 8) fail(SRBCRS_EINVAL, "the merged-window grid takes windows_per_wave 4 or 8");
+      if (!srbcrs::merged_setting_ok(cols, W, ro.depth))
+        fail(SRBCRS_EINVAL, "the merged-window grid runs 8 windows per wave only at wg_cols 64 and depth 2");
       if (vec != 4) fail(SRBCRS_EINVAL, "the merged-window grid needs N, ldb, ldc multiples of 64 / 4 / 4 and "
                                         "16-byte aligned B and C");
       if (!srbcrs::merged_chunks_ok((int)(N / cols)))
@@ -1358,7 +1361,7 @@ int srbcrs_plan_tune(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
   if (reps < 1 || reps > 100) return guarded([&] { fail(SRBCRS_EINVAL, "reps must be in [1, 100] (got %d)", reps); });
   hipStream_t st = static_cast<hipStream_t>(stream);
   plan->tuned.erase(N);
-  std::vector<srbcrs_run_opts> cand;
+  std::vector<srbcrs_run_opts> cand, merged_cand;
   // block fill decides the A source outright at the extremes (measured: compact wins by 14-20 %
   // at 6 % fill, dense by 13 % at 100 %), so only the middle band times both
   const int64_t positions = plan->total * (int64_t)plan->blk_h * plan->blk_w;
@@ -1393,6 +1396,21 @@ int srbcrs_plan_tune(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
         o.b_stage = SRBCRS_B_LDS;
         cand.push_back(o);
       }
+    if (plan->sched.policy == "row" && a == SRBCRS_A_COMPACT && plan->blk_h == 16)
+      // merged windows: each wave walks 4 or 8 windows' blocks interleaved,
+      // its column chunk pinned to one XCD (runs only where N, the leading
+      // dimensions and alignment allow it; others are skipped below)
+      for (const auto& mw : {std::array<int32_t, 3>{128, 4, 4}, std::array<int32_t, 3>{128, 4, 2},
+                             std::array<int32_t, 3>{64, 8, 2}, std::array<int32_t, 3>{64, 4, 4}})
+        if (N % mw[0] == 0 && srbcrs::merged_chunks_ok((int)(N / mw[0]))) {
+          srbcrs_run_opts o{};
+          o.wg_cols = mw[0];
+          o.windows_per_wave = mw[1];
+          o.depth = mw[2];
+          o.grid_order = SRBCRS_GRID_MERGED;
+          o.a_operand = a;
+          merged_cand.push_back(o);
+        }
     if (plan->sched.policy == "row")
       // several consecutive windows per wave: fewer waves than resident
       // slots, all sweeping their windows' columns in step
@@ -1408,6 +1426,10 @@ int srbcrs_plan_tune(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
             cand.push_back(o);
           }
   }
+  // merged-window candidates last (a near-tie keeps the plainer setting); one
+  // the operands cannot run (B / C alignment, ldb / ldc) is dropped here
+  const size_t n_plain = cand.size();
+  cand.insert(cand.end(), merged_cand.begin(), merged_cand.end());
   hipEvent_t e0 = nullptr, e1 = nullptr;
   int rc = guarded([&] {
     hip_check(hipEventCreate(&e0), "hipEventCreate");
@@ -1416,6 +1438,10 @@ int srbcrs_plan_tune(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
   std::vector<float> ms_of(cand.size(), -1.f);
   for (size_t i = 0; rc == SRBCRS_OK && i < cand.size(); ++i) {
     rc = srbcrs_run_ex(plan, d_B, K, N, ldb, d_C, ldc, c_rows, &cand[i], stream);   // warm-up, validates
+    if (rc == SRBCRS_EINVAL && i >= n_plain) {   // a merged setting these operands cannot run
+      rc = SRBCRS_OK;
+      continue;
+    }
     if (rc != SRBCRS_OK) break;
     rc = guarded([&] { hip_check(hipEventRecord(e0, st), "hipEventRecord"); });
     for (int r = 0; rc == SRBCRS_OK && r < reps; ++r)

@@ -87,9 +87,10 @@ hipError_t launch_row_compact(const StreamArgs& a, const int* soff, int Mo, int 
                               hipStream_t st);
 hipError_t launch_tasks_compact(const StreamArgs& a, const TaskTable& t, int vec, const RunOpts& o,
                                 hipStream_t st);
-// spmm_merged: cols 64 (W 4 or 8) or 128 (W 4), depth 2 or 4, vector width 4,
-// a.N / cols column chunks, which merged_chunks_ok must accept.
+// spmm_merged at a setting merged_setting_ok accepts, vector width 4, a.N /
+// cols column chunks, which merged_chunks_ok must accept.
 hipError_t launch_merged(const MergedArgs& m, const StreamArgs& a, int cols, int depth, hipStream_t st);
+bool merged_setting_ok(int cols, int W, int depth);
 bool merged_chunks_ok(int n_chunks);
 hipError_t launch_reduce(const ReduceArgs& a, int vec, hipStream_t st);
 hipError_t launch_csr(const CsrArgs& a, int vec, hipStream_t st);

@@ -34,14 +34,21 @@ static hipError_t launch_merged_t(const MergedArgs& m, const StreamArgs& a, hipS
   return hipGetLastError();
 }
 
-// cols: 64 or 128 columns per wave; W: 4 or 8 windows (8 windows of 128
-// columns hold 256 accumulator registers: one wave per SIMD); depth 2 or 4.
+// cols 64 or 128 columns per wave, W 4 or 8 windows, depth 2 or 4, with 8
+// windows only at 64 columns and depth 2: 8 windows of 128 columns (256
+// accumulator registers) or a 4-deep ring beside 8 windows' tiles spill
+// to scratch.
+bool merged_setting_ok(int cols, int W, int depth) {
+  if (cols != 64 && cols != 128) return false;
+  if (depth != 2 && depth != 4) return false;
+  if (W == 4) return true;
+  return W == 8 && cols == 64 && depth == 2;
+}
+
 hipError_t launch_merged(const MergedArgs& m, const StreamArgs& a, int cols, int depth, hipStream_t st) {
-  if (cols == 64) {
-    if (m.W == 8) return depth == 4 ? launch_merged_t<1, 8, 4>(m, a, st) : launch_merged_t<1, 8, 2>(m, a, st);
-    return depth == 4 ? launch_merged_t<1, 4, 4>(m, a, st) : launch_merged_t<1, 4, 2>(m, a, st);
-  }
-  if (m.W == 8) return depth == 4 ? launch_merged_t<2, 8, 4>(m, a, st) : launch_merged_t<2, 8, 2>(m, a, st);
+  if (!merged_setting_ok(cols, m.W, depth)) return hipErrorInvalidValue;
+  if (m.W == 8) return launch_merged_t<1, 8, 2>(m, a, st);
+  if (cols == 64) return depth == 4 ? launch_merged_t<1, 4, 4>(m, a, st) : launch_merged_t<1, 4, 2>(m, a, st);
   return depth == 4 ? launch_merged_t<2, 4, 4>(m, a, st) : launch_merged_t<2, 4, 2>(m, a, st);
 }
 

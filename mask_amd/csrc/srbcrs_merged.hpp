@@ -64,9 +64,13 @@ __device__ __forceinline__ bool xcd_chunk(int64_t bid, int n_chunks, int64_t n_g
 // every round but the last refills every slot unconditionally with a unit
 // that exists (rounds are whole), and the last round refills only the slots
 // still needed.  Null units are loaded from B row 0 and skipped by a
-// wave-uniform branch.
+// wave-uniform branch.  One group per wave: the tiles are stored once, at
+// the wave's end.  (Waves that streamed several groups and stored each
+// group's tiles between them were slower, 0.243 against 0.215 ms on
+// uniform-65536: vmcnt counts stores with loads, so the ring's next waits
+// also waited for the stores.)
 template <int VEC, int G, int W, int DEPTH, class AF>
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W * G > 8 ? 1 : 2))) void spmm_merged(
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void spmm_merged(
     const int* __restrict__ moff, int Mo, const int* __restrict__ sidx, AF asrc, const float* __restrict__ B,
     float* __restrict__ C, const int* __restrict__ rowmap, int M, int N, int64_t ldb, int64_t ldc, int n_chunks,
     int64_t n_groups) {
@@ -100,7 +104,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(W * G > 8 ? 
     bool live[DEPTH];
     const int64_t last = ue - 1;
     // B rows of a unit; a null unit (indices -1) reads row 0
-    auto rows_of = [&](const UnitRows& r) {
+    auto rows_of = [k](const UnitRows& r) {
       const int2 p = r.pick(k);
       return int2{p.x > 0 ? p.x : 0, p.y > 0 ? p.y : 0};
     };

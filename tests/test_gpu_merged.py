@@ -7,8 +7,6 @@ rows of packed plans, and refuses what it cannot run before launching
 anything."""
 from __future__ import annotations
 
-import itertools
-
 import numpy as np
 import pytest
 
@@ -17,7 +15,7 @@ from tests.helpers import assert_gate, gate, random_csr
 pytestmark = pytest.mark.gpu
 
 MERGED = 4
-SETTINGS = [(64, 8), (64, 4), (128, 4), (128, 8)]   # (wg_cols, windows per group)
+SETTINGS = [(64, 8, 2), (64, 4, 2), (64, 4, 4), (128, 4, 2), (128, 4, 4)]   # (wg_cols, windows per group, depth)
 
 
 def _say(*a):
@@ -47,7 +45,7 @@ def test_merged_bitwise_equals_row_kernel(gpu, M, K, N, density, seed):
     _say("merged", M, K, N)
     ref = plan.run(dB).cpu().numpy()
     assert_gate(gate(ref, rowptr, colind, values, B, M))
-    for (wg, W), depth in itertools.product(SETTINGS, (2, 4)):
+    for wg, W, depth in SETTINGS:
         ch = N // wg
         if N % wg or ch == 0 or (ch > 8 and ch % 8) or (ch < 8 and 8 % ch):
             continue
@@ -113,6 +111,8 @@ def test_merged_refusals_leave_c_untouched(gpu):
         (128, dict(wg_cols=128, windows_per_wave=2), "windows_per_wave"),
         (128, dict(wg_cols=256, windows_per_wave=4), "wg_cols"),
         (128, dict(wg_cols=64, windows_per_wave=8, depth=8), "depth"),
+        (128, dict(wg_cols=64, windows_per_wave=8, depth=4), "8 windows"),
+        (128, dict(wg_cols=128, windows_per_wave=8), "8 windows"),
         (128, dict(wg_cols=64, windows_per_wave=8, a_operand="dense"), "compact"),
         (96, dict(wg_cols=64, windows_per_wave=4), "multiples of 64"),
     ]
@@ -130,3 +130,34 @@ def test_merged_refusals_leave_c_untouched(gpu):
         plan.run(torch.ones((K, 64), device="cuda"), out, grid_order=MERGED, wg_cols=64, windows_per_wave=8)
     torch.cuda.synchronize()
     assert bool((out == 7.0).all())
+
+
+def test_merged_many_generations(gpu):
+    """A grid of several generations of resident waves with runs of empty
+    groups and groups of very different block counts (many null units):
+    bits equal the row kernel's on every row, and a row sample passes the
+    oracle gate."""
+    import torch
+    rng = np.random.default_rng(3)
+    M = K = 72000
+    counts = rng.integers(0, 9, size=M)
+    counts[16 * 100:16 * 140] = 0           # 40 empty windows: whole empty groups
+    rowptr = np.zeros(M + 1, np.int64)
+    rowptr[1:] = np.cumsum(counts)
+    colind = np.concatenate([np.sort(rng.choice(K, c, replace=False)) for c in counts]).astype(np.int32)
+    values = rng.uniform(-1, 1, colind.size).astype(np.float32)
+    rowptr = rowptr.astype(np.int32)
+    N = 512
+    dB = torch.from_numpy(rng.uniform(-1, 1, (K, N)).astype(np.float32)).cuda()
+    plan = _plan(rowptr, colind, values, M)
+    _say("merged persistent", M, N)
+    ref = plan.run(dB).cpu().numpy()
+    for wg, W, depth in SETTINGS:
+        out = torch.full((M, N), float("nan"), device="cuda")
+        plan.run(dB, out, depth=depth, wg_cols=wg, grid_order=MERGED, windows_per_wave=W)
+        assert np.array_equal(out.cpu().numpy(), ref), (wg, W, depth)
+    rows = np.sort(rng.choice(M, 2048, replace=False))
+    sub = ref[rows]
+    rp = np.concatenate([[0], np.cumsum(counts[rows])]).astype(np.int32)
+    idx = np.concatenate([np.arange(rowptr[r], rowptr[r + 1]) for r in rows])
+    assert_gate(gate(sub, rp, colind[idx], values[idx], dB.cpu().numpy(), rows.size))
