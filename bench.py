@@ -72,6 +72,11 @@ def parse():
                     help="block-value copy the kernel reads (default: compact when blocks are at most half full)")
     ap.add_argument("--copy-seconds", type=float, default=0.0,
                     help="with --copy-calibration-mb: repeat the copy for this long")
+    ap.add_argument("--lean", action="store_true",
+                    help="profiling runs: skip the stream / gather probes and the library-tuned leg")
+    ap.add_argument("--umc-seconds", type=float, default=0.0,
+                    help="only measure HBM traffic at the memory controllers: amd-smi UMC activity sampled while a "
+                         "1 GiB copy and then the workload (its published setting) run back to back this long each")
     ap.add_argument("--gather-study", action="store_true",
                     help="only time the gather probe on the workload's own B-row index stream: unit order vs "
                          "units of W windows merged by column, over grids and column-chunk widths")
@@ -188,22 +193,28 @@ def gather_time(rows, row_off, rpi, B, ldb, n_chunks, mapping, reps=20):
 
 
 def gather_ceiling(n_lines=1 << 24, seed=7):
-    """What random gathers out of the L2 move on this box: n_lines uniformly
-    random 128-byte lines (eight per 1 KB load instruction) of a 134 MB
-    buffer, which the 256 MB memory-side cache holds, and of a 2.1 GB buffer,
-    which it does not; and the same bytes as random 1 KB row segments of the
-    134 MB buffer.  One XCD's 4 MB L2 holds 3 % of the smaller buffer, so
-    nearly every line leaves the L2: the rate is the L2-miss gather path's.
-    GB/s of gathered bytes (best of the XCD-blocked and dispatch-order grids)."""
+    """What gathers out of the L2 move on this box: n_lines uniformly random
+    128-byte lines (eight per 1 KB load instruction) of a 134 MB buffer,
+    which the 256 MB memory-side cache holds, and of a 2.1 GB buffer, which
+    it does not; the same bytes as random 1 KB row segments of the 134 MB
+    buffer; and as 1 KB segments read in address order (the path's streaming
+    rate, the highest of the four).  One XCD's 4 MB L2 holds 3 % of the
+    smaller buffer, so nearly every line leaves the L2: the rates are the
+    L2-miss path's.  GB/s of gathered bytes (best of the XCD-blocked and
+    dispatch-order grids)."""
     import torch
     rng = np.random.default_rng(seed)
     out = {}
-    for name, mib, rpi in (("mall_128B", 128, 8), ("hbm_128B", 2048, 8), ("mall_1KB", 128, 1)):
+    for name, mib, rpi in (("mall_128B", 128, 8), ("hbm_128B", 2048, 8), ("mall_1KB", 128, 1),
+                           ("mall_seq_1KB", 128, 1)):
         seg = 256 // rpi
         B = torch.ones(mib * (1 << 20) // 4, device="cuda")
         n_rows_b = B.numel() // seg
         n = n_lines * 128 // (seg * 4)
-        rows = rng.integers(0, n_rows_b, size=n, dtype=np.int64).astype(np.int32)
+        if name.startswith("mall_seq"):   # the same bytes read in address order: the L2-miss path's streaming rate
+            rows = (np.arange(n, dtype=np.int64) % n_rows_b).astype(np.int32)
+        else:
+            rows = rng.integers(0, n_rows_b, size=n, dtype=np.int64).astype(np.int32)
         per = 2048 if rpi == 1 else 4096
         row_off = np.arange(0, n + 1, per, dtype=np.int64)
         best = 0.0
@@ -311,6 +322,210 @@ def gcn_forward_bench(args):
         "spmm_ms": {"N256": round(sp256, 4), "N64": round(sp64, 4)},
         "spmm_gflops": {"N256": round(2 * m.nnz * 256 / sp256 / 1e6, 1), "N64": round(2 * m.nnz * 64 / sp64 / 1e6, 1)},
     }), flush=True)
+
+
+def _find_key(obj, key):
+    """The first value under `key` anywhere in a nested JSON object."""
+    if isinstance(obj, dict):
+        if key in obj:
+            return obj[key]
+        obj = list(obj.values())
+    if isinstance(obj, list):
+        for v in obj:
+            r = _find_key(v, key)
+            if r is not None:
+                return r
+    return None
+
+
+def _pct(v):
+    if isinstance(v, dict):
+        v = v.get("value")
+    try:
+        return float(v)
+    except (TypeError, ValueError):
+        return None
+
+
+def umc_measure(args):
+    """HBM traffic of the workload's steady state, measured at the memory
+    controllers: no per-kernel counter separates memory-side-cache (MALL)
+    hits from HBM accesses, but the SMU's UMC activity sees only HBM.  A
+    thread samples `amd-smi metric -u --json` (gfx and UMC activity, %)
+    while, for args.umc_seconds each, a 1 GiB copy (torch.mul, known bytes)
+    and then the workload at its published setting run back to back.  Only
+    samples with gfx activity >= 99 % count.  The copy's bytes per second
+    over its UMC activity give the GB/s of one UMC percent; the workload's
+    HBM bytes per step = its activity x that scale x its step time.  One
+    JSON line."""
+    import subprocess
+    import threading
+    import torch
+    from mask_amd import datasets
+    from mask_amd.SRBCRSSpMM import Plan
+    samples, stop = [], threading.Event()
+
+    def sampler():
+        while not stop.is_set():
+            t = time.perf_counter()
+            try:
+                txt = subprocess.run(["amd-smi", "metric", "-u", "--json"], capture_output=True, text=True,
+                                     timeout=20).stdout
+                j = json.loads(txt[min(i for i in (txt.find("{"), txt.find("[")) if i >= 0):])
+                g, u = _pct(_find_key(j, "gfx_activity")), _pct(_find_key(j, "umc_activity"))
+                if g is not None and u is not None:
+                    samples.append((t, g, u))
+            except Exception as e:   # a missing or failing amd-smi leaves no samples; reported below
+                samples.append((t, None, repr(e)[:200]))
+                stop.wait(1.0)
+            stop.wait(0.25)
+
+    def phase(fn, seconds):
+        t0 = time.perf_counter()
+        n = 0
+        while time.perf_counter() - t0 < seconds:
+            for _ in range(20):
+                fn()
+            n += 20
+            torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        good = [u for (t, g, u) in samples if g is not None and t0 + 0.5 <= t <= t1 and g >= 99]
+        return n, t1 - t0, good
+
+    th = threading.Thread(target=sampler, daemon=True)
+    th.start()
+    a = torch.ones((1 << 30) // 4, device="cuda")
+    b = torch.empty_like(a)
+    n_c, s_c, u_c = phase(lambda: torch.mul(a, 1.0, out=b), args.umc_seconds)
+    copy_gbs = 2 * a.numel() * 4 * n_c / s_c / 1e9
+    del a, b
+    m = datasets.make_config(args.config)
+    k = dict(PUBLISHED_KNOBS[m.name])
+    N = k.pop("N", 512)
+    dev = torch.device("cuda", 0)
+    t = lambda x: torch.from_numpy(x).to(dev)
+    plan = Plan(t(m.rowptr), t(m.colind), t(m.values), m.M)
+    sched = "split" if m.name in ("rmat-2^20", "gcn-232965") else "row"
+    plan.set_schedule(sched, 0)
+    B = t(m.dense(N))
+    C = torch.empty((m.M, N), device=dev)
+    for _ in range(5):
+        plan.run(B, C, **k)
+    n_w, s_w, u_w = phase(lambda: plan.run(B, C, **k), args.umc_seconds)
+    stop.set()
+    th.join(timeout=30)
+    errors = sorted({u for (t, g, u) in samples if g is None})
+    med = lambda v: float(np.median(v)) if v else None
+    uc, uw = med(u_c), med(u_w)
+    scale = copy_gbs / uc if uc else None
+    ms = s_w / n_w * 1e3
+    out = {"workload": m.name, "N": N, "knobs": k, "schedule": sched, "seconds_each": args.umc_seconds,
+           "copy": {"gbs": round(copy_gbs, 1), "umc_pct": uc, "samples": len(u_c)},
+           "workload_run": {"steps": n_w, "ms_per_step": round(ms, 5), "umc_pct": uw, "samples": len(u_w),
+                            "umc_pct_values": sorted(set(u_w))},
+           "gbs_per_umc_pct": round(scale, 2) if scale else None,
+           "hbm_gbs": round(uw * scale, 1) if scale and uw is not None else None,
+           "hbm_bytes_per_step": int(uw * scale * 1e9 * ms / 1e3) if scale and uw is not None else None,
+           "sampler_errors": errors[:3]}
+    print(json.dumps(out), flush=True)
+
+
+def gcn_forward_measure(args, ceiling=None, settle_s=0.0):
+    """BASELINE config 5 as one step: the GCN workload's two-layer forward
+    relu(A (X W1)) -> A (H W2) on one GPU (X 232965 x 512, W1 512 x 256, W2
+    256 x 64): dense GEMMs through torch (hipBLASLt, fp32) and both SR-BCRS
+    SpMMs (split schedule; N = 256 at the published setting, N = 64 at the
+    library's tuned choice), timed as one step with HIP events, then each
+    part on its own.  Each SpMM carries its roofline block and the fp64
+    oracle gate on a row sample of its own input.  Returns the result dict."""
+    import torch
+    from mask_amd import datasets
+    from mask_amd.gcn import glorot_weights
+    from mask_amd.SRBCRSSpMM import Plan
+    dev = torch.device("cuda", 0)
+    m = datasets.make_config("gcn-232965")
+    gen = torch.Generator(device="cpu")
+    gen.manual_seed(m.seed)
+    X = torch.randn((m.M, 512), generator=gen).to(dev)
+    w1, w2 = glorot_weights([512, 256, 64], seed=m.seed, device=dev)
+    t = lambda a: torch.from_numpy(a).to(dev)
+    plan = Plan(t(m.rowptr), t(m.colind), t(m.values), m.M)
+    plan.set_schedule("split", 0)
+    k256 = {k: v for k, v in PUBLISHED_KNOBS["gcn-232965"].items() if k != "N"}
+    XW = torch.empty((m.M, 256), device=dev)
+    H = torch.empty((m.M, 256), device=dev)
+    HW = torch.empty((m.M, 64), device=dev)
+    out = torch.empty((m.M, 64), device=dev)
+    torch.mm(X, w1, out=XW)
+    plan.run(XW, H, **k256)
+    torch.relu_(H)
+    torch.mm(H, w2, out=HW)
+    k64 = plan.tune(HW, out)   # the N = 64 aggregation at the library's own choice
+
+    parts = {
+        "gemm_xw1": lambda: torch.mm(X, w1, out=XW),
+        "spmm_n256": lambda: plan.run(XW, H, **k256),
+        "relu": lambda: torch.relu_(H),
+        "gemm_hw2": lambda: torch.mm(H, w2, out=HW),
+        "spmm_n64": lambda: plan.run(HW, out),
+    }
+
+    def fwd():
+        for f in parts.values():
+            f()
+
+    for _ in range(args.warmup):
+        fwd()
+    torch.cuda.synchronize()
+    warm = args.warmup
+    t_set = time.perf_counter()
+    while time.perf_counter() - t_set < settle_s:
+        for _ in range(10):
+            fwd()
+        warm += 10
+        torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(args.steps):
+        fwd()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    part_ms = {name: round(_time_ms(f, args.steps, 2), 5) for name, f in parts.items()}
+    M, nnz = m.M, m.nnz
+    flops = {"gemm_xw1": 2.0 * M * 512 * 256, "spmm_n256": 2.0 * nnz * 256, "gemm_hw2": 2.0 * M * 256 * 64,
+             "spmm_n64": 2.0 * nnz * 64}
+    nb, Mo = plan.total_blocks, plan.row_windows
+    spmm = {}
+    for name, N, knobs in (("spmm_n256", 256, dict(k256, tile_b=0)), ("spmm_n64", 64, dict(k64, tile_b=0))):
+        knobs.setdefault("b_stage", "registers")
+        ts = part_ms[name] / 1e3
+        comp = nb * (8 * 4 + 128 * 4) + 4 * (Mo + 1) + m.K * N * 4 + M * N * 4
+        prof = measured_profile(m.name, N, "srbcrs", knobs)
+        spmm[name] = {"N": N, "ms": part_ms[name], "gflops": round(flops[name] / ts / 1e9, 1),
+                      "knobs": {k: knobs[k] for k in ("depth", "wg_cols", "grid_order", "windows_per_wave",
+                                                      "a_operand", "b_stage")},
+                      "roofline": roofline(ts, algorithmic_bytes(M, N, Mo, nb, nnz, "srbcrs"), comp,
+                                           2.0 * 16 * 8 * nb * N, prof, BOUND.get(m.name, "hbm"), ceiling)}
+    parity = {}
+    if not args.no_check:
+        plan.run(XW, H, **k256)        # without the relu: the SpMM's own output
+        parity["spmm_n256"] = parity_leg(m, XW.cpu().numpy(), H.cpu().numpy())
+        plan.run(HW, out)
+        parity["spmm_n64"] = parity_leg(m, HW.cpu().numpy(), out.cpu().numpy())
+    total = sum(flops.values())
+    res = {"value": round(total / (ms / 1e3) / 1e9, 2), "unit": "GFLOP/s", "steps": args.steps, "warmup": warm,
+           "ms_per_step": round(ms, 5),
+           "config": {"workload": GCN_FORWARD, "nodes": M, "nnz": nnz, "features": 512, "hidden": 256, "out": 64,
+                      "schedule": f"{plan.policy[0]}:{plan.policy[1]}", "seed": m.seed,
+                      "flops": {k: int(v) for k, v in flops.items()},
+                      "gemm": "torch.mm fp32 (hipBLASLt)"},
+           "parts_ms": part_ms, "spmm": spmm, "parity": parity}
+    del plan, X, XW, H, HW, out
+    torch.cuda.empty_cache()
+    return res
 
 
 def _time_ms(fn, steps, warmup):
@@ -478,7 +693,8 @@ def algorithmic_bytes(M, N, Mo, nb, nnz, kernel, bh=16, bw=8):
 # every run times the same kernel instantiation as the committed rocprofv3 profile of that workload;
 # --tune times the candidates on the box instead.
 PUBLISHED_KNOBS = {
-    "uniform-65536": {"depth": 2, "wg_cols": 256, "grid_order": 1, "windows_per_wave": 8, "a_operand": "compact"},
+    # merged windows: 4 windows' blocks interleaved per 128-column wave, column chunks pinned to XCDs
+    "uniform-65536": {"depth": 4, "wg_cols": 128, "grid_order": 4, "windows_per_wave": 4, "a_operand": "compact"},
     "banded-524288": {"depth": 2, "wg_cols": 256, "grid_order": 1, "windows_per_wave": 1, "a_operand": "dense"},
     # B staged through LDS by direct-to-LDS loads
     "rmat-2^20": {"depth": 4, "wg_cols": 64, "grid_order": 3, "windows_per_wave": 1, "a_operand": "compact",
@@ -486,9 +702,16 @@ PUBLISHED_KNOBS = {
     # GCN aggregation at the workload's own width (N = 256), split schedule
     "gcn-232965": {"N": 256, "depth": 2, "wg_cols": 64, "grid_order": 3, "windows_per_wave": 1, "a_operand": "compact"},
 }
+# What bounds each workload, from the measurements under profiles/: banded moves its compulsory
+# bytes through HBM at 61 % memory-controller activity (umc_activity_*.md); the others run far below
+# the HBM rate, bound by the gathers' requests out of the L2 (most served by the memory-side cache).
+BOUND = {"banded-524288": "hbm", "uniform-65536": "l2-miss gather path", "rmat-2^20": "l2-miss gather path",
+         "gcn-232965": "l2-miss gather path"}
 # the other large configurations (banded: the second north-star target; R-MAT and the GCN
 # aggregation at N = 256), measured in the same invocation as the headline
 EXTRA_CONFIGS = ("banded-524288", "rmat-2^20", "gcn-232965")
+# ... and BASELINE config 5 as stated: the GCN workload's whole two-layer forward
+GCN_FORWARD = "gcn-232965-forward"
 # Each extra configuration warms for at least this long before its K timed steps (its "warmup"
 # field gives the count): banded's clock boosts, dips and settles within the first ~20 ms of a
 # new load, and K = 20 steps right after 5 warm-up steps land inside that dip.
@@ -518,26 +741,36 @@ def main():
         gather_study(args)
         return
 
-    result = measure(args, args.config, mtx=args.mtx)
-    streams = copy_bandwidth()
-    copy_gbs = streams["copy"]
-    result["roofline"]["stream_gbs"] = streams
-    if result["roofline"].get("frac") is not None:
-        result["roofline"]["frac_of_copy"] = round(result["roofline"]["achieved"] / copy_gbs, 4)
+    if args.umc_seconds > 0:
+        umc_measure(args)
+        return
+    probes_out = {}
+
+    def run_probes():
+        # the stream and gather probes run after the workload's set-up, right
+        # before its W warm-up steps: the GPU then enters the timed steps from
+        # load, not from the idle time of the host-side generation and conversion
+        probes_out["streams"] = copy_bandwidth()
+        probes_out["ceiling"] = gather_ceiling()
+        return probes_out["ceiling"]
+
+    result = measure(args, args.config, mtx=args.mtx, before_warmup=None if args.lean else run_probes)
+    ceiling = probes_out.get("ceiling")
+    if not args.lean:
+        result["roofline"]["stream_gbs"] = probes_out["streams"]
+        result["roofline"]["gather_ceiling"] = ceiling
     default_run = (args.config == "uniform-65536" and not args.mtx and not args.extra_off and args.N in (None, 512)
                    and not explicit_knobs(args)
                    and args.kernel == "srbcrs" and args.blk == "16x8" and args.row_order == "identity")
     if default_run:
         result["extra_configs"] = {}
         for name in EXTRA_CONFIGS:
-            extra = measure(args, name, cpu_seconds=max(3.0, args.cpu_seconds / 2), settle_s=EXTRA_SETTLE_S)
-            extra["roofline"]["stream_gbs"] = streams
-            if extra["roofline"].get("frac") is not None:
-                extra["roofline"]["frac_of_copy"] = round(extra["roofline"]["achieved"] / copy_gbs, 4)
+            extra = measure(args, name, cpu_seconds=max(3.0, args.cpu_seconds / 2), settle_s=EXTRA_SETTLE_S,
+                            ceiling=ceiling)
             result["extra_configs"][name] = {k: extra[k] for k in (
                 "value", "unit", "steps", "warmup", "ms_per_step", "ms_per_step_median", "config", "roofline",
-                "sustained", "parity",
-                "cpu_baseline") if k in extra}
+                "sustained", "library_tuned", "parity", "cpu_baseline") if k in extra}
+        result["extra_configs"][GCN_FORWARD] = gcn_forward_measure(args, ceiling, settle_s=EXTRA_SETTLE_S)
     print(json.dumps(result), flush=True)
 
 
@@ -546,7 +779,7 @@ def explicit_knobs(args):
                 or args.a_operand != "default" or args.b_stage != "default")
 
 
-def measure(args, config, mtx=None, cpu_seconds=None, settle_s=0.0):
+def measure(args, config, mtx=None, cpu_seconds=None, settle_s=0.0, ceiling=None, before_warmup=None):
     """Time one workload (K steps after W warm-up steps, HIP events on the
     launch stream), check it against the oracle on a row sample and time the
     CPU baseline.  Returns the result dict."""
@@ -604,7 +837,15 @@ def measure(args, config, mtx=None, cpu_seconds=None, settle_s=0.0):
     else:
         step = lambda: csr_spmm(rowptr_d, colind_d, values_d, B, m.M, max_col=max_col, out=C)
 
-    for _ in range(args.warmup):
+    n_warm = args.warmup
+    if before_warmup is not None and n_warm > 0:
+        # the first warm-up step prepares what the plan builds on first use
+        # (the merged-window stream), then the probes run, then the rest
+        step()
+        torch.cuda.synchronize()
+        n_warm -= 1
+        ceiling = before_warmup()
+    for _ in range(n_warm):
         step()
     torch.cuda.synchronize()
     warmup_done = args.warmup
@@ -672,10 +913,12 @@ def measure(args, config, mtx=None, cpu_seconds=None, settle_s=0.0):
         e1.record(stream)
         torch.cuda.synchronize()
         ms_s = e0.elapsed_time(e1) / n_s
-        rs = roofline(ms_s / 1e3, ab, compulsory, padded_flops, prof)
+        rs = roofline(ms_s / 1e3, ab, compulsory, padded_flops, prof, BOUND.get(m.name, "hbm"), ceiling)
         sustained = {"steps": n_s, "seconds": round(ms_s * n_s / 1e3, 3), "ms_per_step": round(ms_s, 5),
                      "value": round(flops / (ms_s / 1e3) / 1e9, 2), "frac": rs["frac"],
-                     "compulsory_frac": rs["compulsory_frac"]}
+                     "hbm_frac": rs["hbm_frac"]}
+        if "gather_frac" in rs:
+            sustained["gather_frac"] = rs["gather_frac"]
 
     result = {
         "metric": "SpMM GFLOP/s at N=512 fp32 on 1 MI355X; % of HBM roofline",
@@ -697,11 +940,24 @@ def measure(args, config, mtx=None, cpu_seconds=None, settle_s=0.0):
                    "schedule": f"{plan.policy[0]}:{plan.policy[1]}", "seed": m.seed, "row_order": args.row_order,
                    "conversion_s": round(conv_s, 3), "meta": m.meta,
                    "knobs": knobs},
-        "roofline": roofline(t_s, ab, compulsory, padded_flops, prof),
+        "roofline": roofline(t_s, ab, compulsory, padded_flops, prof, BOUND.get(m.name, "hbm"), ceiling),
         "wall_s_timed": round(wall, 4),
     }
     if sustained is not None:
         result["sustained"] = sustained
+
+    if knobs.get("source") == "bench.PUBLISHED_KNOBS" and not args.lean:
+        # beside the published setting: what the library picks for itself on
+        # this plan (srbcrs_plan_tune, the drop-in's autotune), timed the same way
+        t0 = time.time()
+        tk = plan.tune(B, C)
+        torch.cuda.synchronize()
+        tune_s = time.time() - t0
+        ms_t = _time_ms(lambda: plan.run(B, C), args.steps, args.warmup)
+        same = all(str(tk[k]) == str(knobs[k]) for k in ("depth", "wg_cols", "grid_order", "windows_per_wave",
+                                                          "a_operand", "b_stage"))
+        result["library_tuned"] = {"knobs": tk, "tune_s": round(tune_s, 3), "ms_per_step": round(ms_t, 5),
+                                   "value": round(flops / (ms_t / 1e3) / 1e9, 2), "same_as_published": same}
 
     budget = args.cpu_seconds if cpu_seconds is None else cpu_seconds
     if not (args.no_check and args.no_cpu):
@@ -716,38 +972,59 @@ def measure(args, config, mtx=None, cpu_seconds=None, settle_s=0.0):
     return result
 
 
-def roofline(t_s, dataflow_bytes, compulsory_bytes, padded_flops, prof):
-    """The HBM roofline block of a result.
+def roofline(t_s, dataflow_bytes, compulsory_bytes, padded_flops, prof, bound="hbm", gather_ceiling=None):
+    """The roofline block of a result.
 
-    frac = achieved / peak, achieved = HBM-side bytes per launch / step time.
-    The bytes are the measured ones when a committed profile of this exact
-    launch setting exists (prof: DRAM-destined read and write requests out of
-    the L2, rocprofv3 TCC_EA0_RDREQ_DRAM_32B / TCC_EA0_WRREQ_WRITE_DRAM_32B,
-    calibrated on a copy kernel; memory-side-cache hits are included, since no
-    per-kernel counter separates them), else the compulsory bytes (A as stored,
-    B once, C once).  Either is a byte count the memory system must move, so
-    the fraction is bounded by the peak; a fraction above 1 means the bytes
-    are wrong, and the bench then reports null rather than the figure.  The
-    SR-BCRS dataflow bytes (every B row gathered per block, reads that the L2
-    also serves) are reported as dataflow_gbs, not as a fraction."""
-    if prof is not None:
-        hbm_bytes, basis = prof["dram_bytes"], f"measured: {prof['file']} (DRAM-destined L2 requests)"
-    else:
-        hbm_bytes, basis = compulsory_bytes, "compulsory bytes (no profile of this launch setting)"
-    achieved = hbm_bytes / t_s / 1e9
+    frac = achieved / peak with achieved = compulsory bytes per step (A as
+    stored, B once, C once: the bytes any schedule must move) / step time,
+    against the 8 TB/s HBM peak.  Beside it, each from its own source:
+      hbm_bytes       bytes that reached HBM, measured at the memory
+                      controllers (amd-smi UMC activity) for this launch
+                      setting (prof "hbm_bytes_umc"), else the compulsory
+                      bytes; hbm_basis names which;
+      l2_egress_bytes requests out of the L2 toward the memory side
+                      (TCC_EA0_*_DRAM counters, prof "l2_egress_bytes"):
+                      memory-side-cache hits included, so never an HBM figure;
+      traffic         FETCH_SIZE + WRITE_SIZE of the same profile (also L2
+                      egress);
+      gather_frac     L2-egress rate / the gather ceiling (random line
+                      gathers out of the L2 on the same box, gather_ceiling());
+      dataflow_gbs    every gathered B row per block over the step time: a
+                      rate only (the L2 serves part of it).
+    A compulsory fraction above 1 would mean the byte model is wrong: frac is
+    then null and frac_rejected holds it."""
+    achieved = compulsory_bytes / t_s / 1e9
     frac = achieved / HBM_PEAK_GBS
-    out = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+    prof = prof or {}
+    if prof.get("hbm_bytes_umc"):
+        hbm, hbm_basis = prof["hbm_bytes_umc"], f"memory-controller (UMC) activity: {prof['file']}"
+    else:
+        hbm, hbm_basis = compulsory_bytes, "compulsory bytes (no memory-controller measurement of this setting)"
+    out = {"bound": bound, "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
            "frac": round(frac, 4) if frac <= 1.0 else None,
-           "basis": basis, "hbm_bytes": int(hbm_bytes),
-           "traffic": prof["traffic_bytes"] if prof else None,
+           "basis": "compulsory bytes (A as stored + B once + C once) / step time",
+           "traffic": prof.get("traffic_bytes"),
+           "traffic_basis": ("FETCH_SIZE + WRITE_SIZE, copy-calibrated: bytes leaving the L2, memory-side-cache "
+                             f"hits included ({prof['file']})") if prof.get("traffic_bytes") else None,
            "compulsory_bytes": int(compulsory_bytes),
-           "compulsory_frac": round(compulsory_bytes / t_s / 1e9 / HBM_PEAK_GBS, 4),
+           "hbm_bytes": int(hbm), "hbm_basis": hbm_basis,
+           "hbm_frac": round(hbm / t_s / 1e9 / HBM_PEAK_GBS, 4),
            "dataflow_bytes": int(dataflow_bytes), "dataflow_gbs": round(dataflow_bytes / t_s / 1e9, 1),
            "mfma_padded_tflops": round(padded_flops / t_s / 1e12, 3),
            "mfma_frac": round(padded_flops / t_s / 1e12 / FP32_MFMA_PEAK_TFLOPS, 4)}
     if frac > 1.0:
         out["frac_rejected"] = round(frac, 4)
-    if prof is not None and prof.get("kernel_avg_ms"):
+    if prof.get("l2_egress_bytes"):
+        eg = prof["l2_egress_bytes"] / t_s / 1e9
+        out.update({"l2_egress_bytes": int(prof["l2_egress_bytes"]), "l2_egress_gbs": round(eg, 1),
+                    "l2_egress_frac": round(eg / HBM_PEAK_GBS, 4),
+                    "l2_egress_basis": f"TCC_EA0_RDREQ_DRAM_32B + TCC_EA0_WRREQ_WRITE_DRAM_32B, copy-calibrated "
+                                       f"({prof['file']})"})
+        if gather_ceiling:
+            c = max(gather_ceiling.values())
+            out["gather_ceiling_gbs"] = c
+            out["gather_frac"] = round(eg / c, 4)
+    if prof.get("kernel_avg_ms"):
         out["profile_kernel_avg_ms"] = prof["kernel_avg_ms"]
     return out
 
@@ -755,25 +1032,26 @@ def roofline(t_s, dataflow_bytes, compulsory_bytes, padded_flops, prof):
 def measured_profile(workload, N, kernel, knobs, blk="16x8"):
     """The committed rocprofv3 summary of this workload whose "knobs:" line
     (block shape included; 16x8 when the line names none) matches the launch
-    settings of this run: {"file", "dram_bytes", "traffic_bytes",
-    "kernel_avg_ms"}, or None when there is none or it lacks a dram_bytes line."""
+    settings of this run: {"file", "l2_egress_bytes", "traffic_bytes",
+    "kernel_avg_ms", "hbm_bytes_umc" (when measured)}, or None when there is
+    none or it lacks an l2_egress_bytes line."""
     if kernel != "srbcrs" or knobs is None:
         return None
     want = {k: str(knobs[k]) for k in ("depth", "wg_cols", "grid_order", "windows_per_wave", "a_operand")}
     want["blk"] = blk
     want["b_stage"] = str(knobs.get("b_stage", "registers"))
-    for path in sorted((ROOT / "profiles").glob(f"spmm_stream_{workload.replace('^', '')}_N{N}*.md")):
+    for path in sorted((ROOT / "profiles").glob(f"spmm_*_{workload.replace('^', '')}_N{N}*.md")):
         fields, prof_knobs = {}, None
         for line in path.read_text().splitlines():
             key, _, val = line.partition(":")
-            if key in ("traffic_bytes", "dram_bytes"):
+            if key in ("traffic_bytes", "l2_egress_bytes", "hbm_bytes_umc"):
                 fields[key] = int(val)
             elif key == "kernel_avg_ns":
                 fields["kernel_avg_ms"] = round(int(val) / 1e6, 5)
             elif key == "knobs":
                 prof_knobs = dict(kv.split("=") for kv in val.split())
         if prof_knobs and {"windows_per_wave": "1", "blk": "16x8", "b_stage": "registers", **prof_knobs} == want \
-                and "dram_bytes" in fields:
+                and "l2_egress_bytes" in fields:
             return {"file": f"profiles/{path.name}", "traffic_bytes": fields.get("traffic_bytes"), **fields}
     return None
 
@@ -807,6 +1085,14 @@ def _check_sample(oracle, m, B_host, C, n_rows=4096):
     met["rows_checked"] = int(rows.size)
     met["pass"] = bool(met["finite"] and met["max_ratio"] <= 1e-4 and met["ref_gate"])
     return met
+
+
+def parity_leg(m, B_host, C):
+    """The correctness gate of one SpMM result C (host array, all rows) with
+    dense input B_host against the fp64 oracle on a seeded row sample (the
+    CPU leg's checker, for results that have no CPU-baseline timing)."""
+    from oracle import oracle
+    return _check_sample(oracle, m, B_host, C)
 
 
 def cpu_baseline_leg(m, B_host, N, budget_s, C=None, time_baseline=True):

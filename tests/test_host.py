@@ -370,12 +370,12 @@ def test_bench_byte_model_and_traffic_lookup():
     assert bench.algorithmic_bytes(M, N, Mo, nb // 8, 0, "srbcrs", 32, 32) == \
         4 * (Mo + 1) + nb // 8 * (32 * 4 + 1024 * 4) + nb // 8 * 32 * N * 4 + M * N * 4
     assert bench.algorithmic_bytes(10, 64, 1, 1, 100, "csr") == 4 * 11 + 8 * 100 + 4 * 64 * 100 + 4 * 10 * 64
-    knobs = dict(bench.PUBLISHED_KNOBS["uniform-65536"], tile_b=0, b_stage="registers")
-    got = bench.measured_profile("uniform-65536", 512, "srbcrs", knobs)
-    assert got is not None and got["dram_bytes"] > 0 and got["file"].startswith("profiles/")
-    assert bench.measured_profile("uniform-65536", 512, "srbcrs", {**knobs, "depth": 3}) is None
-    assert bench.measured_profile("uniform-65536", 512, "csr", knobs) is None
-    assert bench.measured_profile("uniform-65536", 512, "srbcrs", knobs, "32x32") is None
+    knobs = dict(bench.PUBLISHED_KNOBS["banded-524288"], tile_b=0, b_stage="registers")
+    got = bench.measured_profile("banded-524288", 512, "srbcrs", knobs)
+    assert got is not None and got["l2_egress_bytes"] > 0 and got["file"].startswith("profiles/")
+    assert bench.measured_profile("banded-524288", 512, "srbcrs", {**knobs, "depth": 3}) is None
+    assert bench.measured_profile("banded-524288", 512, "csr", knobs) is None
+    assert bench.measured_profile("banded-524288", 512, "srbcrs", knobs, "32x32") is None
 
 
 def test_bench_reports_the_library_default_a_operand():
@@ -441,39 +441,53 @@ def test_operand_checks_raise_before_any_launch():
 
 
 def test_bench_roofline_is_bounded():
-    """bench.roofline never reports a fraction above 1: bytes that imply more
-    than the HBM peak over the step time are rejected (frac null), and the
-    dataflow bytes (gathers served by the caches) are reported as a rate only."""
+    """bench.roofline: frac is the compulsory bytes over the step time against
+    the 8 TB/s peak (null above 1); the dataflow bytes are a rate only."""
     import bench
     t = 1e-3
-    ok = bench.roofline(t, dataflow_bytes=9e9, compulsory_bytes=2e9, padded_flops=1e10,
-                        prof={"file": "p.md", "dram_bytes": 6_000_000_000, "traffic_bytes": 6_100_000_000})
-    assert ok["frac"] == 0.75 and ok["hbm_bytes"] == 6_000_000_000 and ok["dataflow_gbs"] == 9000.0
-    assert ok["compulsory_frac"] == 0.25 and ok["basis"].startswith("measured")
-    bad = bench.roofline(t, dataflow_bytes=9e9, compulsory_bytes=2e9, padded_flops=1e10,
-                         prof={"file": "p.md", "dram_bytes": 9_000_000_000, "traffic_bytes": None})
+    ok = bench.roofline(t, dataflow_bytes=9e9, compulsory_bytes=2e9, padded_flops=1e10, prof=None)
+    assert ok["frac"] == 0.25 and ok["achieved"] == 2000.0 and ok["dataflow_gbs"] == 9000.0
+    assert ok["basis"].startswith("compulsory")
+    bad = bench.roofline(t, dataflow_bytes=9e9, compulsory_bytes=9e9, padded_flops=1e10, prof=None)
     assert bad["frac"] is None and bad["frac_rejected"] == 1.125
-    fallback = bench.roofline(t, 9e9, 2e9, 1e10, None)
-    assert fallback["frac"] == 0.25 and fallback["basis"].startswith("compulsory")
+
+
+def test_bench_l2_egress_never_feeds_hbm_bytes():
+    """A profile whose only byte figure is the L2-egress counters (TCC_EA0 *
+    DRAM requests, which include memory-side-cache hits) must not become the
+    HBM bytes: those come only from a memory-controller (UMC) measurement;
+    without one the HBM bytes are the compulsory bytes, and the basis says so."""
+    import bench
+    t = 1e-3
+    prof = {"file": "profiles/p.md", "l2_egress_bytes": 6_000_000_000, "traffic_bytes": 6_100_000_000}
+    r = bench.roofline(t, 9e9, 2e9, 1e10, prof, bound="l2-miss gather path", gather_ceiling={"a": 7000.0, "b": 7500.0})
+    assert r["hbm_bytes"] == 2_000_000_000 and r["hbm_basis"].startswith("compulsory")
+    assert r["l2_egress_bytes"] == 6_000_000_000 and r["l2_egress_frac"] == 0.75
+    assert r["gather_ceiling_gbs"] == 7500.0 and r["gather_frac"] == 0.8
+    assert r["frac"] == 0.25 and r["bound"] == "l2-miss gather path"
+    umc = bench.roofline(t, 9e9, 2e9, 1e10, dict(prof, hbm_bytes_umc=1_000_000_000))
+    assert umc["hbm_bytes"] == 1_000_000_000 and "UMC" in umc["hbm_basis"] and umc["hbm_frac"] == 0.125
+    assert umc["frac"] == 0.25   # the headline fraction keeps its compulsory basis
 
 
 def test_committed_profiles_are_physical():
-    """Every committed kernel profile with measured DRAM bytes implies at most
-    the 8 TB/s HBM peak over its own kernel average, and bench.py finds the
-    profile of each published launch setting."""
+    """Every committed kernel profile's L2-egress and UMC-measured HBM bytes
+    imply at most the 8 TB/s peak over its own kernel average, and bench.py
+    finds the profile of each published launch setting."""
     import bench
     from pathlib import Path
     found = 0
-    for path in sorted((Path(bench.ROOT) / "profiles").glob("spmm_stream_*.md")):
+    for path in sorted((Path(bench.ROOT) / "profiles").glob("spmm_*.md")):
         fields = dict(l.split(":", 1) for l in path.read_text().splitlines()
-                      if l.startswith(("dram_bytes:", "kernel_avg_ns:")))
-        if "dram_bytes" in fields:
-            found += 1
-            gbs = int(fields["dram_bytes"]) / int(fields["kernel_avg_ns"])
-            assert gbs <= bench.HBM_PEAK_GBS, (path.name, gbs)
+                      if l.startswith(("l2_egress_bytes:", "hbm_bytes_umc:", "kernel_avg_ns:")))
+        for key in ("l2_egress_bytes", "hbm_bytes_umc"):
+            if key in fields:
+                found += 1
+                gbs = int(fields[key]) / int(fields["kernel_avg_ns"])
+                assert gbs <= bench.HBM_PEAK_GBS, (path.name, key, gbs)
     assert found >= 1
     for name, knobs in bench.PUBLISHED_KNOBS.items():
         k = dict({key: v for key, v in knobs.items() if key != "N"}, tile_b=0)
         k.setdefault("b_stage", "registers")
         prof = bench.measured_profile(name, knobs.get("N", 512), "srbcrs", k)
-        assert prof is not None and prof["dram_bytes"] > 0, name
+        assert prof is not None and prof["l2_egress_bytes"] > 0, name
