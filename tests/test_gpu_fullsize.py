@@ -101,7 +101,7 @@ def _workload(name):
     return _WORKLOADS[name]
 
 
-@pytest.mark.parametrize("name", ["banded-524288", "rmat-2^20", "gcn-232965"])
+@pytest.mark.parametrize("name", ["uniform-65536", "banded-524288", "rmat-2^20", "gcn-232965"])
 def test_full_size_conversion_bit_exact(gpu, name):
     """The default device converter (radix sort on the GPU) against the host
     converter of the same CSR and against the oracle, byte for byte, on the

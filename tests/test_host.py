@@ -4,6 +4,7 @@ the Python drop-in module's argument checks."""
 from __future__ import annotations
 
 import ctypes
+import os
 import re
 from pathlib import Path
 
@@ -31,6 +32,47 @@ def test_library_exports_every_declared_symbol():
     for n in names:
         assert hasattr(L, n), n
     assert b"gfx950" in L.srbcrs_version()
+
+
+def test_loader_refuses_experiment_builds(tmp_path):
+    """A decomposition build (results wrong on purpose) carries
+    "+experiment:<name>" in srbcrs_version(); the product loader refuses it
+    unless MASK_AMD_ALLOW_EXPERIMENT=1.  Built here as a stamped C-ABI object
+    linked with the product's other objects."""
+    import shutil
+    import subprocess
+    import sys
+    from mask_amd import build as B
+    objs = [B.PKG / "_build" / (s.rsplit(".", 1)[0] + ".o") for s in B.SOURCES if s != "srbcrs_capi.cpp"]
+    if not all(o.exists() for o in objs) or not shutil.which(B._hipcc()):
+        pytest.skip("library objects not built")
+    capi = tmp_path / "capi_stamped.o"
+    B._run([B._hipcc(), *B.DEVICE_FLAGS, "-DSRBCRS_EXPERIMENT_TAG=loader_check", f"-I{ROOT / 'include'}", "-x", "hip",
+            "-c", str(B.CSRC / "srbcrs_capi.cpp"), "-o", str(capi)])
+    lib = tmp_path / "libmask_srbcrs_loader_check.so"
+    B._run([B._hipcc(), f"--offload-arch={B.ARCH}", "-shared", "-fPIC", "-o", str(lib), str(capi), *map(str, objs),
+            "-lpthread"])
+    code = "from mask_amd import _capi; print(_capi.lib().srbcrs_version().decode())"
+    env = dict(os.environ, MASK_AMD_SRBCRS_LIB=str(lib))
+    env.pop("MASK_AMD_ALLOW_EXPERIMENT", None)
+    r = subprocess.run([sys.executable, "-c", code], cwd=ROOT, env=env, capture_output=True, text=True)
+    assert r.returncode != 0 and "decomposition build" in r.stderr, r.stderr[-500:]
+    env["MASK_AMD_ALLOW_EXPERIMENT"] = "1"
+    r = subprocess.run([sys.executable, "-c", code], cwd=ROOT, env=env, capture_output=True, text=True)
+    assert r.returncode == 0 and "+experiment:loader_check" in r.stdout, r.stderr[-500:]
+    assert "+experiment:" not in _capi.lib().srbcrs_version().decode()
+
+
+def test_probe_entry_points_stay_out_of_the_public_abi():
+    """The measurement probes are exported by the library (bench.py binds
+    them) but declared only in the internal header, not in include/srbcrs.h."""
+    import bench
+    public = _header_functions()
+    L = _capi.lib()
+    for name in bench.PROBE_SIGS:
+        assert name not in public and hasattr(L, name), name
+    internal = (ROOT / "mask_amd" / "csrc" / "srbcrs_probe.h").read_text()
+    assert all(name in internal for name in bench.PROBE_SIGS)
 
 
 def _same(a, b):
