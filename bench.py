@@ -229,10 +229,12 @@ def gather_ceiling(n_lines=1 << 24, seed=7):
 
 def gather_study(args):
     """Gather-only timings (srbcrs_gather_probe) of the workload's own B-row
-    index stream at N = 512, printed as one JSON line: the kernel's unit order
-    (windows_per_wave W, 1 KB segments, the XCD-blocked chunk-major grid), and
-    the units of W windows merged by first column, with column chunks of 64,
-    128 or 256 columns pinned to XCDs (chunk = XCD % chunks)."""
+    index stream at N = 512, printed as one JSON line.  Groups are row
+    windows, or for the skewed graphs (R-MAT, GCN) segments of at most 64
+    units of a window, as the split schedule cuts them; W consecutive groups
+    go to one wave, in unit order or merged by first B-row index; column
+    chunks of 32 to 256 columns; grids: dispatch-order chunk sweep (0), the
+    XCD-blocked chunk-major grid (1), or chunks pinned to XCDs (2)."""
     import torch
     from mask_amd import _capi, datasets
     m = datasets.make_config(args.config)
@@ -241,25 +243,38 @@ def gather_study(args):
     N = 512
     B = torch.from_numpy(m.dense(N)).cuda()
     nb = sidx.shape[0]
+    skewed = m.name in ("rmat-2^20", "gcn-232965")
     win = np.repeat(np.arange(soff.size - 1), np.diff(soff))
+    if skewed:   # segments of at most 64 units of one window
+        pos = np.arange(nb) - soff[win]
+        seg_key = win * 1_000_000 + pos // 64
+        _, seg = np.unique(seg_key, return_inverse=True)
+    else:
+        seg = win
+    if skewed:
+        runs = [(1, False, 4, 0), (1, False, 4, 1), (1, False, 4, 2), (4, True, 4, 0), (8, True, 4, 0),
+                (1, False, 8, 0), (1, False, 2, 0), (1, False, 1, 0), (1, False, 1, 1), (4, True, 4, 2)]
+    else:
+        runs = [(8, False, 1, 1), (8, False, 4, 2), (8, True, 1, 2), (8, True, 2, 2), (8, True, 4, 2),
+                (4, True, 2, 2), (4, True, 4, 2), (16, True, 4, 2), (32, True, 4, 2), (1, False, 4, 2),
+                (1, False, 1, 1)]
     res = []
-    for W, merge, rpi, mapping in ((8, False, 1, 1), (8, False, 4, 2), (8, True, 1, 2), (8, True, 2, 2),
-                                   (8, True, 4, 2), (4, True, 2, 2), (4, True, 4, 2), (16, True, 4, 2),
-                                   (32, True, 4, 2), (1, False, 4, 2), (1, False, 1, 1)):
-        grp = win // W
+    for W, merge, rpi, mapping in runs:
+        grp = seg // W
         perm = np.lexsort((np.arange(nb), sidx[:, 0], grp)) if merge else np.arange(nb)
         rows = sidx[perm].ravel()
         row_off = np.zeros(grp.max() + 2, np.int64)
         np.add.at(row_off, grp + 1, 8)
         row_off = np.cumsum(row_off)
         n_chunks = N // (256 // rpi)
-        ms, nbytes = gather_time(rows, row_off, rpi, B, N, n_chunks, mapping)
+        if mapping == 2 and 8 % n_chunks and n_chunks % 8:
+            continue
+        ms, nbytes = gather_time(rows, row_off, rpi, B, N, n_chunks, mapping, reps=5 if skewed else 20)
         r = {"W": W, "merged": merge, "cols": 256 // rpi, "mapping": mapping, "ms": round(ms, 4),
              "gbs": round(nbytes / ms / 1e6, 1)}
         print("[gather-study]", r, file=sys.stderr, flush=True)
         res.append(r)
-    print(json.dumps({"workload": m.name, "N": N, "gathered_bytes": int(nb * 8 * N * 4), "runs": res,
-                      "ceiling": gather_ceiling()}), flush=True)
+    print(json.dumps({"workload": m.name, "N": N, "gathered_bytes": int(nb * 8 * N * 4), "runs": res}), flush=True)
 
 
 def gcn_forward_bench(args):

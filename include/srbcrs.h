@@ -84,7 +84,7 @@ typedef struct srbcrs_plan_desc {
   int32_t dup_policy;     /* SRBCRS_DUP_* */
   int64_t stored_values;  /* values in the compact copy of val (-1: no copy) */
   const void *d_a_words;  /* compact copy: one {mask, base} uint32 pair per 32 block positions (NULL: none) */
-  const float *d_a_packed; /* compact copy: the stored values in logical order */
+  const float *d_a_packed; /* compact copy: the stored values in logical order, then 16 zero floats */
 } srbcrs_plan_desc;
 int srbcrs_plan_get(const srbcrs_plan *plan, srbcrs_plan_desc *out);
 

@@ -122,8 +122,12 @@ hipError_t device_compact(const float* val, int64_t n_blocks, int blk_h, int blk
   SRBCRS_STEP(hipMemcpyAsync(h_tail, tail, 8, hipMemcpyDeviceToHost, st));
   SRBCRS_STEP(hipStreamSynchronize(st));
   out.n_packed = (int64_t)h_tail[0] + h_tail[1];
-  out.packed = (float*)alloc(ctx, (size_t)(out.n_packed > 0 ? out.n_packed : 1) * 4);
+  // kPackedPad zero floats after the stored values: the SpMM reads packed[n]
+  // and packed[n + 1] unconditionally (n <= n_packed) and selects, so that
+  // its loads do not sit in lane-divergent branches
+  out.packed = (float*)alloc(ctx, (size_t)(out.n_packed + kPackedPad) * 4);
   if (!out.packed) return fail(hipErrorOutOfMemory);
+  SRBCRS_STEP(hipMemsetAsync(out.packed + out.n_packed, 0, kPackedPad * 4, st));
   hipLaunchKernelGGL(k_word_fill, dim3(grid_for(n_pos)), dim3(256), 0, st, val, n_pos, block_size, bases,
                      out.words, out.packed);
   SRBCRS_STEP(hipGetLastError());

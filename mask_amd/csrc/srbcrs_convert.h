@@ -36,9 +36,13 @@ hipError_t device_convert(const DeviceConvertIn& in, DeviceConvertOut& out, Devi
 
 // Compact copy of the block values (srbcrs_compact.hip): per 32 logical
 // positions of a block one {mask, base} word, and the stored values.
+// Zero floats allocated after the stored values (CompactA reads packed[n]
+// and packed[n + 1] for n <= n_packed without a branch).
+constexpr int64_t kPackedPad = 16;
+
 struct CompactOut {
   uint2* words = nullptr;   // n_blocks * BH*BW/32
-  float* packed = nullptr;  // n_packed (at least one element allocated)
+  float* packed = nullptr;  // n_packed stored values, then kPackedPad zeros
   int64_t n_packed = 0;
 };
 

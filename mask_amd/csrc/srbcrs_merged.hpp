@@ -34,6 +34,12 @@
 #pragma once
 #include "srbcrs_stream.hpp"
 
+#ifdef SRBCRS_MERGED_SCHED_PIN
+#define SRBCRS_MERGED_PIN __builtin_amdgcn_sched_barrier(0)
+#else
+#define SRBCRS_MERGED_PIN (void)0
+#endif
+
 namespace srbcrs {
 
 // Workgroup id -> (window group g, column chunk c) with the chunk pinned to
@@ -126,12 +132,14 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sp
       for (int j = 0; j < W; ++j) {
         const int d = j % DEPTH;
         if (live[d]) mma_frag<1, VEC, G>(f[d], acc[j]);
+        SRBCRS_MERGED_PIN;
         const int64_t nu = base + j + DEPTH;   // exists: a whole round follows this one
         live[d] = idx[d].lo.x >= 0;
         load_frag<BH, BW, VEC, G>(f[d], B, asrc, nu, rows_of(idx[d]), am[d], a_off, ldb, col0, lane);
         const int64_t nn = nu + DEPTH < last ? nu + DEPTH : last;
         idx[d].load(sidx, nn);
         am[d] = asrc.template meta<BH, BW>(nn, lane);
+        SRBCRS_MERGED_PIN;
       }
     }
     // the last round: refill only the slots whose next unit is in it

@@ -103,7 +103,8 @@ struct Frag {
 // low block fills of graph matrices most of the dense array is zeros, so
 // this cuts the A bytes a column chunk re-reads by up to ~10x.  The word is
 // fetched one ring slot ahead (Meta), so the value loads it steers issue
-// with the unit's B loads.
+// with the unit's B loads.  `packed` must hold at least one readable float
+// past its last stored value (srbcrs_compact.hip pads it with zeros).
 struct DenseA {
   const float* __restrict__ val;
   template <int H> struct Meta {};
@@ -172,8 +173,15 @@ struct CompactA {
       v0 = (float)n;
       v1 = (float)(b0 + b1);
 #else
-      if (b0) v0 = packed[n];
-      if (b1) v1 = packed[n + b0];
+      // Both loads are issued on every lane and the absent values are
+      // selected away: n + b0 <= the stored-value count, and the array holds
+      // a few zero floats after the last one.  As loads inside lane-divergent
+      // branches their number was unknown to the compiler, which then waited
+      // for the next unit's B rows before issuing this refill (vmcnt counted
+      // for the fewest loads on any path).
+      const float p0 = packed[n], p1 = packed[n + b0];
+      v0 = b0 ? p0 : 0.f;
+      v1 = b1 ? p1 : 0.f;
 #endif
       a[h] = f2{v0, v1};
     }
