@@ -77,6 +77,9 @@ def parse():
     ap.add_argument("--umc-seconds", type=float, default=0.0,
                     help="only measure HBM traffic at the memory controllers: amd-smi UMC activity sampled while a "
                          "1 GiB copy and then the workload (its published setting) run back to back this long each")
+    ap.add_argument("--window-sharing", action="store_true",
+                    help="host only: distinct (row window, column) pairs at window heights 16..256, i.e. how many "
+                         "B-row gathers windows of more rows would share")
     ap.add_argument("--gather-study", action="store_true",
                     help="only time the gather probe on the workload's own B-row index stream: unit order vs "
                          "units of W windows merged by column, over grids and column-chunk widths")
@@ -733,8 +736,25 @@ GCN_FORWARD = "gcn-232965-forward"
 EXTRA_SETTLE_S = 1.0
 
 
+def window_sharing(args):
+    """How many B-row gathers neighbouring row windows share (host only):
+    the number of distinct (row // h, column) pairs of the workload for
+    window heights h = 16 .. 256, against h = 16 (the SR-BCRS window, one
+    gather per pair and column chunk).  One JSON line."""
+    from mask_amd import datasets
+    m = datasets.make_config(args.config)
+    rows = np.repeat(np.arange(m.M, dtype=np.int64), np.diff(m.rowptr))
+    cols = m.colind.astype(np.int64)
+    out = {h: int(np.unique((rows // h) * (1 << 21) + cols).size) for h in (16, 32, 64, 128, 256)}
+    print(json.dumps({"workload": m.name, "nnz": m.nnz, "distinct_pairs": out,
+                      "ratio_to_16": {h: round(v / out[16], 4) for h, v in out.items()}}), flush=True)
+
+
 def main():
     args = parse()
+    if args.window_sharing:
+        window_sharing(args)
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print(json.dumps({"error": "this benchmark measures one GPU; --gpus must be 1 "
                                    "(the SpMM path is single-GPU, sharding is design-only)"}))
