@@ -197,6 +197,9 @@ def test_full_size_integer_protocol_exact(gpu, name):
     runs = [(("row", 0), {}), (("split", 0), {}), (("auto", 0), {})]
     if name == "rmat-2^20":
         runs.append((("split", 0), dict(depth=4, wg_cols=64, grid_order=3, b_stage="lds")))
+    # the merged-window grid on the row schedule (N = 64: one 64-column chunk)
+    runs.append((("row", 0), dict(depth=2, wg_cols=64, grid_order=4, windows_per_wave=8)))
+    runs.append((("row", 0), dict(depth=4, wg_cols=64, grid_order=4, windows_per_wave=4)))
     for sched, knobs in runs:
         _say("  schedule", sched, knobs)
         plan.set_schedule(*sched)
