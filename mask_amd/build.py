@@ -144,6 +144,7 @@ EXPERIMENTS = {
     "b_skip_two_thirds": "SRBCRS_EXPERIMENT_B_SKIP=3",  # only every 3rd unit gathers B (register ring)
     "lds_pad_40k": "SRBCRS_EXPERIMENT_LDS_PAD=40960",    # 40 KB of unused LDS per workgroup: at most 4 per CU
     "merged_pin": "SRBCRS_MERGED_SCHED_PIN",            # merged grid: loads pinned in source order (sched_barrier)
+    "merged_vec_idx": "SRBCRS_MERGED_VEC_IDX",          # merged grid: each lane loads its B-row index pair
 }
 
 

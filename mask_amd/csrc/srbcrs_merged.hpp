@@ -42,6 +42,31 @@
 
 namespace srbcrs {
 
+// The B-row indices of one unit for the lane.  By default all 8 are read
+// wave-uniformly (scalar loads) and the lane picks its pair; with
+// SRBCRS_MERGED_VEC_IDX each lane loads its own pair (one 8-byte vector load,
+// no selects), counted on vmcnt with the ring's other loads.
+#ifdef SRBCRS_MERGED_VEC_IDX
+struct MergedRows {
+  int2 p;
+  __device__ __forceinline__ void load(const int* __restrict__ sidx, int64_t unit, int k) {
+    p = *reinterpret_cast<const int2*>(sidx + unit * 8 + 2 * k);
+  }
+  __device__ __forceinline__ bool live() const { return __builtin_amdgcn_readfirstlane(p.x) >= 0; }
+  __device__ __forceinline__ int2 rows(int) const { return int2{p.x > 0 ? p.x : 0, p.y > 0 ? p.y : 0}; }
+};
+#else
+struct MergedRows {
+  UnitRows r;
+  __device__ __forceinline__ void load(const int* __restrict__ sidx, int64_t unit, int) { r.load(sidx, unit); }
+  __device__ __forceinline__ bool live() const { return r.lo.x >= 0; }
+  __device__ __forceinline__ int2 rows(int k) const {
+    const int2 q = r.pick(k);
+    return int2{q.x > 0 ? q.x : 0, q.y > 0 ? q.y : 0};
+  }
+};
+#endif
+
 // Workgroup id -> (window group g, column chunk c) with the chunk pinned to
 // the XCD the dispatcher deals the workgroup to (id % 8).  n_chunks divides
 // 8 (XCD x serves chunk x % n_chunks, 8 / n_chunks groups per round of 8
@@ -105,25 +130,21 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sp
     int a_off[1][1];
     a_off[0][0] = swizzle_2_2_3(BW * (lane & 15) + 2 * k);
     Frag<1, VEC, G> f[DEPTH];
-    UnitRows idx[DEPTH];
+    MergedRows idx[DEPTH];
     typename AF::template Meta<1> am[DEPTH];
     bool live[DEPTH];
     const int64_t last = ue - 1;
-    // B rows of a unit; a null unit (indices -1) reads row 0
-    auto rows_of = [k](const UnitRows& r) {
-      const int2 p = r.pick(k);
-      return int2{p.x > 0 ? p.x : 0, p.y > 0 ? p.y : 0};
-    };
+    // a null unit (indices -1) reads B row 0 (MergedRows::rows) and is skipped
 #pragma unroll
     for (int d = 0; d < DEPTH; ++d) {   // rounds hold W >= DEPTH units
       const int64_t u = us + d;
-      UnitRows r;
-      r.load(sidx, u);
-      live[d] = r.lo.x >= 0;
-      load_frag<BH, BW, VEC, G>(f[d], B, asrc, u, rows_of(r), asrc.template meta<BH, BW>(u, lane), a_off, ldb,
+      MergedRows r;
+      r.load(sidx, u, k);
+      live[d] = r.live();
+      load_frag<BH, BW, VEC, G>(f[d], B, asrc, u, r.rows(k), asrc.template meta<BH, BW>(u, lane), a_off, ldb,
                                 col0, lane);
       const int64_t nu = us + DEPTH + d < last ? us + DEPTH + d : last;
-      idx[d].load(sidx, nu);
+      idx[d].load(sidx, nu, k);
       am[d] = asrc.template meta<BH, BW>(nu, lane);
     }
     int64_t base = us;
@@ -134,10 +155,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sp
         if (live[d]) mma_frag<1, VEC, G>(f[d], acc[j]);
         SRBCRS_MERGED_PIN;
         const int64_t nu = base + j + DEPTH;   // exists: a whole round follows this one
-        live[d] = idx[d].lo.x >= 0;
-        load_frag<BH, BW, VEC, G>(f[d], B, asrc, nu, rows_of(idx[d]), am[d], a_off, ldb, col0, lane);
+        live[d] = idx[d].live();
+        load_frag<BH, BW, VEC, G>(f[d], B, asrc, nu, idx[d].rows(k), am[d], a_off, ldb, col0, lane);
         const int64_t nn = nu + DEPTH < last ? nu + DEPTH : last;
-        idx[d].load(sidx, nn);
+        idx[d].load(sidx, nn, k);
         am[d] = asrc.template meta<BH, BW>(nn, lane);
         SRBCRS_MERGED_PIN;
       }
@@ -149,10 +170,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sp
       if (live[d]) mma_frag<1, VEC, G>(f[d], acc[j]);
       if (j + DEPTH < W) {
         const int64_t nu = base + j + DEPTH;
-        live[d] = idx[d].lo.x >= 0;
-        load_frag<BH, BW, VEC, G>(f[d], B, asrc, nu, rows_of(idx[d]), am[d], a_off, ldb, col0, lane);
+        live[d] = idx[d].live();
+        load_frag<BH, BW, VEC, G>(f[d], B, asrc, nu, idx[d].rows(k), am[d], a_off, ldb, col0, lane);
         if (j + 2 * DEPTH < W) {
-          idx[d].load(sidx, nu + DEPTH);
+          idx[d].load(sidx, nu + DEPTH, k);
           am[d] = asrc.template meta<BH, BW>(nu + DEPTH, lane);
         }
       }
