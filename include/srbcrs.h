@@ -246,8 +246,8 @@ int srbcrs_plan_trim(srbcrs_plan *plan, void *stream);
  *                time (its B rows shared through the memory-side cache),
  *                4 = merged windows ("row" schedule, 16x8 blocks with the
  *                compact A copy, vector width 4): one wave per
- *                windows_per_wave windows (4 or 8; 0 = 8) and wg_cols
- *                columns (64 or 128; 0 = 64), walking the
+ *                windows_per_wave windows (4 or 8; 0 = 8 at 64 columns,
+ *                4 at 128) and wg_cols columns (64 or 128; 0 = 64), walking the
  *                windows' blocks interleaved (block r of each window in
  *                turn) so that it sweeps its B rows once in ascending order,
  *                the column chunk pinned to one XCD (N / wg_cols must divide

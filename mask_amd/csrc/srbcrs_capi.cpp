@@ -1184,14 +1184,16 @@ static void run_impl(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
     // the first launch: a refused call leaves C untouched.
     const bool merged = opts && opts->grid_order == SRBCRS_GRID_MERGED;
     if (merged) {
-      const int cols = ro.wg_cols == 128 ? 128 : 64;
-      const int W = opts->windows_per_wave ? opts->windows_per_wave : 8;
+      // merged defaults (knobs left 0): 64-column waves with 8 windows, or 4
+      // windows at 128 columns; depth 2
+      const int cols = opts->wg_cols ? opts->wg_cols : 64;
+      const int W = opts->windows_per_wave ? opts->windows_per_wave : (cols == 64 ? 8 : 4);
       if (plan->sched.policy != "row") fail(SRBCRS_EINVAL, "the merged-window grid runs the \"row\" schedule only");
       if (plan->blk_h != 16 || (!plan->d_awords && plan->total > 0))
         fail(SRBCRS_EINVAL, "the merged-window grid needs 16x8 blocks with the compact copy of the block values");
       if (opts->a_operand == SRBCRS_A_DENSE || opts->b_stage == SRBCRS_B_LDS)
         fail(SRBCRS_EINVAL, "the merged-window grid reads the compact A copy and keeps B in registers");
-      if (ro.wg_cols != 64 && ro.wg_cols != 128) fail(SRBCRS_EINVAL, "the merged-window grid takes wg_cols 64 or 128");
+      if (cols != 64 && cols != 128) fail(SRBCRS_EINVAL, "the merged-window grid takes wg_cols 64 or 128");
       if (ro.depth != 2 && ro.depth != 4) fail(SRBCRS_EINVAL, "the merged-window grid takes depth 2 or 4");
       if (W != 4 && W != 8) fail(SRBCRS_EINVAL, "the merged-window grid takes windows_per_wave 4 or 8");
       if (!srbcrs::merged_setting_ok(cols, W, ro.depth))

@@ -100,6 +100,21 @@ def test_merged_packed_plans(gpu):
         assert_gate(gate(ref, rowptr, colind, values, B, M))
 
 
+def test_merged_default_knobs(gpu):
+    """grid_order 4 with every other knob 0 runs the documented defaults
+    (64-column waves, 8 windows, depth 2) and gives the row kernel's bits."""
+    import torch
+    M, K, N = 500, 900, 256
+    rowptr, colind, values = random_csr(M, K, 0.02, seed=12)
+    plan = _plan(rowptr, colind, values, M)
+    dB = torch.from_numpy(np.random.default_rng(12).uniform(-1, 1, (K, N)).astype(np.float32)).cuda()
+    _say("merged defaults", M, N)
+    ref = plan.run(dB).cpu().numpy()
+    assert np.array_equal(plan.run(dB, grid_order=MERGED).cpu().numpy(), ref)
+    assert np.array_equal(plan.run(dB, grid_order=MERGED, wg_cols=128).cpu().numpy(), ref)   # 128 x 4 windows
+    assert np.array_equal(plan.run(dB, grid_order=MERGED, wg_cols=128, windows_per_wave=4).cpu().numpy(), ref)
+
+
 def test_merged_refusals_leave_c_untouched(gpu):
     import torch
     from mask_amd._capi import SrbcrsError
