@@ -254,7 +254,24 @@ int srbcrs_plan_trim(srbcrs_plan *plan, void *stream);
  *                8 or be a multiple of 8); depth 2 or 4 (8 windows: only
  *                at 64 columns and depth 2).  The first run per
  *                windows_per_wave builds the interleaved copy of the block
- *                indices and A words on the host (it allocates);
+ *                indices and A words on the host (it allocates),
+ *                5 = nonzero sweep: the vector kernel for low block density
+ *                ("row" schedule, 16x8 blocks with the compact A copy).
+ *                One wave per windows_per_wave windows (4, 8 or 16; 0 = 8)
+ *                and 64 columns walks the windows' stored values in the
+ *                merged order (one 256-byte B-row gather and one LDS
+ *                read-add-write per value, no padded block arithmetic);
+ *                tile_b = values per sub-batch (16, 32 or 64; 0 = 32),
+ *                depth = sub-batches of gathers in flight (2 or 4; 0 = 2;
+ *                4 only with tile_b 16 or 32); wg_cols 0 or 64.  Needs N a
+ *                multiple of 64 with N / 64 dividing 8 or a multiple of 8,
+ *                ldb and ldc multiples of 4, 16-byte aligned B and C,
+ *                K * ldb * 4 < 2^32, ldb * 4 < 2^24 and column indices
+ *                below 2^23.  C[r, :] is the sum of fl(v * B[c, :]) over
+ *                the row's stored values in ascending column order, each
+ *                product rounded before it is added (the fp32 CSR product,
+ *                not the MFMA kernels' bits).  The first run per setting
+ *                builds its value stream on the host (it allocates);
  *   windows_per_wave  "row" schedule: consecutive row windows one wave
  *                streams through its register ring (0 = 1), in [0, 4096];
  *   a_operand    see SRBCRS_A_* below;
@@ -265,8 +282,10 @@ int srbcrs_plan_trim(srbcrs_plan *plan, void *stream);
  *                double buffer (kernel.inc:584-642) in gfx950 form.  LDS
  *                staging applies at vector width 4 (tile_b 64 and 16-byte
  *                aligned B, ldb % 4 == 0); other launches use registers.
- * Values outside these sets are rejected.  Every setting yields the same
- * bits: the per-element accumulation order does not depend on them. */
+ * Values outside these sets are rejected.  Every MFMA setting (grid orders
+ * 0-4) yields the same bits: the per-element accumulation order does not
+ * depend on them; the nonzero sweep (grid order 5) yields the fp32 CSR
+ * product's bits, equal to the others within fp32 rounding. */
 typedef struct srbcrs_run_opts {
   int32_t depth;
   int32_t tile_b;
@@ -297,6 +316,7 @@ typedef struct srbcrs_run_opts {
 #define SRBCRS_GRID_WINDOW_MAJOR 2
 #define SRBCRS_GRID_CHUNK_SWEEP 3
 #define SRBCRS_GRID_MERGED 4
+#define SRBCRS_GRID_NZSWEEP 5
 
 /* srbcrs_run with explicit knobs (opts NULL = defaults). */
 int srbcrs_run_ex(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int64_t ldb,
@@ -315,7 +335,9 @@ int srbcrs_run_ex(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int
  * that overlap on one GPU (other streams, other threads) race; calls in
  * stream order do not.  Results are bit-identical to srbcrs_run_ex with the
  * same arguments.  The plan's schedule tables must exist already
- * (srbcrs_plan_set_schedule allocates them). */
+ * (srbcrs_plan_set_schedule allocates them), and so must the host-built
+ * stream of a merged-window or nonzero-sweep setting (the first
+ * srbcrs_run_ex with those knobs builds it); otherwise SRBCRS_EINVAL. */
 int srbcrs_run_noalloc(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int64_t ldb,
                        float *d_C, int64_t ldc, int64_t c_rows, const srbcrs_run_opts *opts,
                        void *stream);

@@ -148,7 +148,9 @@ class Plan:
         """out[:num_nodes] = A @ dense on the current stream.  The keyword
         knobs are the kernel template parameters (srbcrs_run_opts; 0 =
         default; grid_order 1 = chunk-major, 2 = window-major, 3 = chunk sweep, 4 = merged
-        windows ("row" schedule: windows_per_wave windows interleaved per wave); a_operand
+        windows ("row" schedule: windows_per_wave windows interleaved per wave), 5 = nonzero
+        sweep (the vector kernel for low block density: one gather per stored value, tile_b
+        values per sub-batch; its bits are the fp32 CSR product's); a_operand
         "compact" / "dense" picks the block-value copy the kernel reads; b_stage
         "registers" / "lds" where the ring holds the gathered B rows)."""
         out = self._operands(dense, out)

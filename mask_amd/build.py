@@ -72,7 +72,7 @@ def build(verbose: bool = False) -> Path:
 
 
 # translation units of the library, the slowest (the spmm_stream instantiations) first
-SOURCES = ("srbcrs_merged.hip", "srbcrs_stream_compact.hip", "srbcrs_stream_compact_tasks.hip", "srbcrs_stream_dense.hip",
+SOURCES = ("srbcrs_merged.hip", "srbcrs_nzsweep.hip", "srbcrs_stream_compact.hip", "srbcrs_stream_compact_tasks.hip", "srbcrs_stream_dense.hip",
            "srbcrs_stream_dense_tasks.hip", "srbcrs_kernels.hip", "srbcrs_capi.cpp", "srbcrs_pack.cpp",
            "srbcrs_convert.hip", "srbcrs_compact.hip", "srbcrs_probe.hip")
 GENERATED = PKG / "generated"

@@ -454,6 +454,14 @@ struct srbcrs_plan {
     int64_t units = 0;
   };
   std::map<int, Merged> merged;
+  // nonzero-sweep streams (spmm_nzsweep), per windows per group W,
+  // sub-batch size U and chunk size (key nz_key)
+  struct Nz {
+    int32_t* d_eoff = nullptr;   // group g's pairs: [eoff[g], eoff[g+1])
+    uint2* d_pairs = nullptr;    // ((B row << 9) | tile row, value bits)
+    int64_t entries = 0;
+  };
+  std::map<int64_t, Nz> nz;
 
   template <class T>
   void retire(T*& p) {
@@ -490,6 +498,10 @@ struct srbcrs_plan {
       dev_free(kv.second.d_moff);
       dev_free(kv.second.d_sidx);
       dev_free(kv.second.d_words);
+    }
+    for (auto& kv : nz) {
+      dev_free(kv.second.d_eoff);
+      dev_free(kv.second.d_pairs);
     }
     if (switched) (void)hipSetDevice(cur);
   }
@@ -724,6 +736,139 @@ const srbcrs_plan::Merged& merged_stream(srbcrs_plan& plan, int W, hipStream_t s
   }
   m.units = units;
   return plan.merged.emplace(W, m).first->second;
+}
+
+int64_t nz_key(int W, int U, int D) { return ((int64_t)W << 16) | ((int64_t)U << 8) | (int64_t)D; }
+
+// The entry stream of the nonzero sweep for groups of W row windows and
+// sub-batches of U entries (spmm_nzsweep, srbcrs_nzsweep.hpp).  A group's
+// stored values are listed in the merged unit order (block r of each window
+// in window order, then r + 1), within a block column by column and, in a
+// column, row by row; each is the entry (B row << 8) | (16 * window slot +
+// row) with its value.  The list is then cut into sub-batches of U entries
+// with distinct tile rows: each sub-batch takes, in list order, the entries
+// among the next 4U not yet taken whose row is neither in the sub-batch nor
+// held by an earlier entry left behind, so every row keeps its values in
+// list order (ascending columns); a sub-batch short of U is filled with
+// entries for tile row 16 * W (never stored) that repeat the previous B row
+// (a cache hit).  Groups are padded the same way to whole chunks (of
+// max(64, U * D) entries: the kernel reads a chunk's entries ahead).
+// Built on the host from the plan's sidx, compact A words and packed values.
+const srbcrs_plan::Nz& nz_stream(srbcrs_plan& plan, int W, int U, int D, hipStream_t st) {
+  const int64_t key = nz_key(W, U, D);
+  auto it = plan.nz.find(key);
+  if (it != plan.nz.end()) return it->second;
+  const int kChunk = 2 * D * U;      // the kernel's loop body
+  const int E = 4, Q = U / E;   // entries per gather instruction, instructions per sub-batch
+  constexpr int kRowBits = 9;
+  constexpr int kWords = 16 * 8 / 32;
+  const int64_t nb = plan.total;
+  const int Mo = plan.Mo;
+  if (plan.max_col >= (1 << (32 - kRowBits)))
+    fail(SRBCRS_EINVAL, "the nonzero sweep takes B-row indices below 2^%d (the matrix references column %d)",
+         32 - kRowBits, plan.max_col);
+  std::vector<int32_t> sidx((size_t)nb * 8);
+  std::vector<uint2> words((size_t)nb * kWords);
+  std::vector<float> packed((size_t)plan.n_apacked);
+  if (nb) {
+    hip_check(hipMemcpyAsync(sidx.data(), plan.d_sidx, sidx.size() * sizeof(int32_t), hipMemcpyDeviceToHost, st),
+              "hipMemcpyAsync sidx D2H");
+    hip_check(hipMemcpyAsync(words.data(), plan.d_awords, words.size() * sizeof(uint2), hipMemcpyDeviceToHost, st),
+              "hipMemcpyAsync A words D2H");
+    if (!packed.empty())
+      hip_check(hipMemcpyAsync(packed.data(), plan.d_apacked, packed.size() * sizeof(float), hipMemcpyDeviceToHost,
+                               st),
+                "hipMemcpyAsync packed values D2H");
+    hip_check(hipStreamSynchronize(st), "hipStreamSynchronize");
+  }
+  const uint32_t dummy = (uint32_t)(16 * W);
+  const int64_t n_groups = (Mo + W - 1) / W;
+  std::vector<std::vector<uint2>> g_pairs((size_t)n_groups);
+  parallel_for(n_groups, [&](int64_t lo, int64_t hi) {
+    std::vector<uint32_t> le;
+    std::vector<float> lv;
+    std::vector<char> taken;
+    for (int64_t g = lo; g < hi; ++g) {
+      // the group's values in list order
+      le.clear();
+      lv.clear();
+      int32_t rounds = 0;
+      for (int64_t win = g * W; win < Mo && win < (g + 1) * W; ++win)
+        rounds = std::max(rounds, plan.h_soff[win + 1] - plan.h_soff[win]);
+      for (int32_t r = 0; r < rounds; ++r)
+        for (int w = 0; w < W; ++w) {
+          const int64_t win = g * W + w;
+          if (win >= Mo) break;
+          const int64_t b = (int64_t)plan.h_soff[win] + r;
+          if (b >= plan.h_soff[win + 1]) continue;
+          for (int k = 0; k < 8; ++k)
+            for (int row = 0; row < 16; ++row) {
+              const int pos = 8 * row + k;
+              const uint2 wd = words[(size_t)b * kWords + (pos >> 5)];
+              const int bit = pos & 31;
+              if (!((wd.x >> bit) & 1u)) continue;
+              le.push_back(((uint32_t)sidx[(size_t)b * 8 + k] << kRowBits) | (uint32_t)(16 * w + row));
+              lv.push_back(packed[(size_t)wd.y + __builtin_popcount(wd.x & ((1u << bit) - 1u))]);
+            }
+        }
+      // sub-batches of U distinct tile rows, each stored transposed: pair
+      // gg * Q + q = entry E * q + gg
+      std::vector<uint2>& op = g_pairs[(size_t)g];
+      std::vector<uint2> batch((size_t)U);
+      const size_t n = le.size();
+      taken.assign(n, 0);
+      size_t head = 0;
+      uint32_t prev = le.empty() ? 0u : le[0] >> kRowBits;
+      auto put = [&](int u, uint32_t e, float v) {
+        batch[(size_t)((u % E) * Q + u / E)] = uint2{e, __builtin_bit_cast(uint32_t, v)};
+      };
+      while (head < n) {
+        uint64_t used[8] = {0, 0, 0, 0, 0, 0, 0, 0}, held[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        int got = 0;
+        for (size_t i = head; i < n && i < head + 4 * (size_t)U && got < U; ++i) {
+          if (taken[i]) continue;
+          const uint32_t t = le[i] & ((1u << kRowBits) - 1u);
+          const uint64_t bit = 1ull << (t & 63);
+          if ((used[t >> 6] | held[t >> 6]) & bit) {
+            held[t >> 6] |= bit;
+            continue;
+          }
+          used[t >> 6] |= bit;
+          taken[i] = 1;
+          put(got, le[i], lv[i]);
+          prev = le[i] >> kRowBits;
+          ++got;
+        }
+        for (; got < U; ++got) put(got, (prev << kRowBits) | dummy, 0.f);
+        op.insert(op.end(), batch.begin(), batch.end());
+        while (head < n && taken[head]) ++head;
+      }
+      while (op.size() % kChunk) op.push_back(uint2{(prev << kRowBits) | dummy, 0u});
+    }
+  });
+  std::vector<int32_t> eoff((size_t)n_groups + 1, 0);
+  int64_t entries = 0;
+  for (int64_t g = 0; g < n_groups; ++g) {
+    entries += (int64_t)g_pairs[(size_t)g].size();
+    if (entries > INT32_MAX) fail(SRBCRS_EINVAL, "the nonzero-sweep stream exceeds 2^31 entries");
+    eoff[(size_t)g + 1] = (int32_t)entries;
+  }
+  std::vector<uint2> pairs((size_t)entries);
+  parallel_for(n_groups, [&](int64_t lo, int64_t hi) {
+    for (int64_t g = lo; g < hi; ++g)
+      std::copy(g_pairs[(size_t)g].begin(), g_pairs[(size_t)g].end(), pairs.begin() + eoff[(size_t)g]);
+  });
+  srbcrs_plan::Nz z;
+  try {
+    z.d_eoff = upload(eoff);
+    z.d_pairs = upload(pairs);
+  } catch (...) {
+    dev_free(z.d_eoff);
+    dev_free(z.d_pairs);
+    throw;
+  }
+  z.entries = entries;
+  return plan.nz.emplace(key, z).first->second;
 }
 
 }  // namespace
@@ -1126,8 +1271,8 @@ static void run_impl(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
         fail(SRBCRS_EINVAL, "tile_b must be 0, 16, 32 or 64 (got %d)", opts->tile_b);
       if (opts->wg_cols != 0 && (opts->wg_cols < 64 || opts->wg_cols > 512 || (opts->wg_cols & (opts->wg_cols - 1))))
         fail(SRBCRS_EINVAL, "wg_cols must be 0 or a power of two in [64, 512] (got %d)", opts->wg_cols);
-      if (opts->grid_order < 0 || opts->grid_order > 4)
-        fail(SRBCRS_EINVAL, "grid_order must be 0, 1, 2, 3 or 4 (got %d)", opts->grid_order);
+      if (opts->grid_order < 0 || opts->grid_order > 5)
+        fail(SRBCRS_EINVAL, "grid_order must be 0, 1, 2, 3, 4 or 5 (got %d)", opts->grid_order);
       if (opts->depth) ro.depth = opts->depth;
       if (opts->wg_cols) ro.wg_cols = opts->wg_cols;
       if (opts->grid_order)
@@ -1211,6 +1356,41 @@ static void run_impl(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
                   "launch zero_rows");
       srbcrs::MergedArgs ma{m.d_moff, plan->Mo, W, m.d_sidx, m.d_words};
       hip_check(srbcrs::launch_merged(ma, a, cols, ro.depth, st), "launch spmm_merged");
+      return;
+    }
+    if (opts && opts->grid_order == SRBCRS_GRID_NZSWEEP) {
+      // defaults (knobs left 0): 8 windows per group, sub-batches of 32
+      // entries, 2 in flight
+      const int W = opts->windows_per_wave ? opts->windows_per_wave : 8;
+      const int U = opts->tile_b ? opts->tile_b : 32;
+      const int D = opts->depth ? opts->depth : 2;
+      if (plan->sched.policy != "row") fail(SRBCRS_EINVAL, "the nonzero sweep runs the \"row\" schedule only");
+      if (plan->blk_h != 16 || (!plan->d_awords && plan->total > 0))
+        fail(SRBCRS_EINVAL, "the nonzero sweep needs 16x8 blocks with the compact copy of the block values");
+      if (opts->a_operand == SRBCRS_A_DENSE || opts->b_stage == SRBCRS_B_LDS)
+        fail(SRBCRS_EINVAL, "the nonzero sweep reads the compact A copy and keeps B in registers");
+      if (opts->wg_cols && opts->wg_cols != 64)
+        fail(SRBCRS_EINVAL, "the nonzero sweep runs 64 columns per wave (got wg_cols %d)", opts->wg_cols);
+      if (!srbcrs::nz_setting_ok(W, U, D))
+        fail(SRBCRS_EINVAL, "the nonzero sweep takes windows_per_wave 4, 8 or 16 and (tile_b, depth) (16, 2), (16, 4) "
+                            "or (32, 2) (got %d, %d, %d)", W, U, D);
+      if (N % 64 || !srbcrs::merged_chunks_ok((int)(N / 64)))
+        fail(SRBCRS_EINVAL, "the nonzero sweep needs N a multiple of 64 with N / 64 column chunks dividing 8 or a "
+                            "multiple of 8");
+      if (N % 4 || ldb % 4 || ldc % 4 || (reinterpret_cast<uintptr_t>(d_B) | reinterpret_cast<uintptr_t>(d_C)) % 16)
+        fail(SRBCRS_EINVAL, "the nonzero sweep needs ldb, ldc multiples of 4 and 16-byte aligned B and C");
+      if ((uint64_t)K * (uint64_t)ldb * 4u >= (1ull << 32) || (uint64_t)ldb * 4u >= (1ull << 24))
+        fail(SRBCRS_EINVAL, "the nonzero sweep addresses B with 32-bit offsets: K * ldb * 4 must stay below 2^32 "
+                            "and ldb * 4 below 2^24");
+      if (fixed_partial && !plan->nz.count(nz_key(W, U, D)))
+        fail(SRBCRS_EINVAL, "the nonzero-sweep stream for %d windows and sub-batches of %d is not built yet: call "
+                            "srbcrs_run_ex once with these knobs first (it allocates)", W, U);
+      const srbcrs_plan::Nz& z = nz_stream(*plan, W, U, D, st);
+      if (plan->n_zero_rows)
+        hip_check(srbcrs::launch_zero_rows(d_C, plan->d_zero_rows, plan->n_zero_rows, (int)N, ldc, st),
+                  "launch zero_rows");
+      srbcrs::NzArgs za{z.d_eoff, plan->Mo, W, z.d_pairs};
+      hip_check(srbcrs::launch_nzsweep(za, a, U, D, st), "launch spmm_nzsweep");
       return;
     }
     if (plan->sched.policy == "row") {

@@ -43,6 +43,16 @@ struct MergedArgs {
   const uint2* words;
 };
 
+// Nonzero-sweep operands (spmm_nzsweep): group g of W row windows owns the
+// (entry, value) pairs [eoff[g], eoff[g+1]), entry = (B row << 9) | tile
+// row, laid out for one launch setting (sub-batch size and ring depth).
+struct NzArgs {
+  const int* eoff;
+  int Mo;
+  int W;
+  const uint2* pairs;
+};
+
 struct TaskTable {
   const int* group_off;
   const int* task_begin;
@@ -92,6 +102,13 @@ hipError_t launch_tasks_compact(const StreamArgs& a, const TaskTable& t, int vec
 hipError_t launch_merged(const MergedArgs& m, const StreamArgs& a, int cols, int depth, hipStream_t st);
 bool merged_setting_ok(int cols, int W, int depth);
 bool merged_chunks_ok(int n_chunks);
+// grid of the merged-window kernels: rounds of 8 workgroups, one per XCD
+int64_t merged_grid(int64_t n_groups, int n_chunks);
+// spmm_nzsweep: W 4, 8 or 16, (U, D) = (tile_b, depth) one of
+// nz_setting_ok's, a.N / 64 column chunks, which merged_chunks_ok must
+// accept.
+hipError_t launch_nzsweep(const NzArgs& z, const StreamArgs& a, int U, int D, hipStream_t st);
+bool nz_setting_ok(int W, int U, int D);
 hipError_t launch_reduce(const ReduceArgs& a, int vec, hipStream_t st);
 hipError_t launch_csr(const CsrArgs& a, int vec, hipStream_t st);
 hipError_t launch_zero_rows(float* C, const int* rows, int n_rows, int N, int64_t ldc, hipStream_t st);

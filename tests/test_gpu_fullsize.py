@@ -87,7 +87,13 @@ def test_full_size_workload(gpu, name, schedule):
     knobs = dict(bench.PUBLISHED_KNOBS.get(name, {}))
     if knobs and knobs.pop("N", 512) == B.shape[1]:
         _say("full", name, "published", knobs)
-        assert torch.equal(plan.run(dB, **knobs), C), knobs
+        got = plan.run(dB, **knobs)
+        if knobs.get("grid_order") == 5:
+            # the nonzero sweep: the fp32 CSR product's bits (every row)
+            want = oracle.csr_spmm_f32(m.rowptr, m.colind, m.values, B, m.M)
+            assert np.array_equal(got.cpu().numpy(), want), knobs
+        else:
+            assert torch.equal(got, C), knobs
 
 
 _WORKLOADS = {}
@@ -173,7 +179,7 @@ def test_full_size_integer_protocol_exact(gpu, name):
     integers -14..14 (14 x its ((i % 29) - 14) / 14, :1341) make every
     partial sum an integer below 2^24, so fp32 is exact in any order and C
     must equal the int64 product bit for bit, on every schedule the bench
-    uses (and the LDS ring)."""
+    uses (and the LDS ring, the merged-window grid and the nonzero sweep)."""
     import scipy.sparse as sp
     import torch
     from mask_amd.SRBCRSSpMM import Plan
@@ -200,6 +206,9 @@ def test_full_size_integer_protocol_exact(gpu, name):
     # the merged-window grid on the row schedule (N = 64: one 64-column chunk)
     runs.append((("row", 0), dict(depth=2, wg_cols=64, grid_order=4, windows_per_wave=8)))
     runs.append((("row", 0), dict(depth=4, wg_cols=64, grid_order=4, windows_per_wave=4)))
+    # the nonzero sweep (its own summation order; exact all the same)
+    runs.append((("row", 0), dict(depth=2, tile_b=32, grid_order=5, windows_per_wave=8)))
+    runs.append((("row", 0), dict(depth=4, tile_b=16, grid_order=5, windows_per_wave=4)))
     for sched, knobs in runs:
         _say("  schedule", sched, knobs)
         plan.set_schedule(*sched)

@@ -1,0 +1,222 @@
+"""GPU parity of the nonzero sweep (grid_order 5, spmm_nzsweep): every legal
+setting equals the CPU oracle's fp32 CSR product (oracle_csr_spmm_f32: each
+product rounded, then added in ascending column order) bit for bit, passes
+the fp64 oracle gate, handles ragged groups (empty windows and rows, a last
+group short of W windows, M % 16 != 0, long rows), row maps and omitted
+rows of packed plans and last-wins duplicates, is deterministic, and refuses
+what it cannot run before launching anything."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import oracle
+from tests.helpers import assert_gate, dedupe_last, gate, random_csr
+
+pytestmark = pytest.mark.gpu
+
+NZ = 5
+SETTINGS = [(W, U, D) for W in (4, 8, 16) for (U, D) in ((16, 2), (16, 4), (32, 2), (32, 4), (64, 2))]
+
+
+def _say(*a):
+    print("[case]", *a, flush=True)
+
+
+def _plan(rowptr, colind, values, M, **kw):
+    import torch
+    from mask_amd.SRBCRSSpMM import Plan
+    t = lambda a: torch.from_numpy(a).cuda()
+    return Plan(t(rowptr), t(colind), t(values), M, **kw)
+
+
+def _run(plan, dB, M, N, W, U, D):
+    import torch
+    out = torch.full((M, N), float("nan"), device="cuda")
+    plan.run(dB, out, grid_order=NZ, windows_per_wave=W, tile_b=U, depth=D)
+    return out.cpu().numpy()
+
+
+@pytest.mark.parametrize("M,K,N,density,seed", [
+    (16 * 37 + 5, 3000, 512, 0.005, 1),     # ragged last window, last group short of W windows
+    (640, 700, 128, 0.03, 2),
+    (257, 257, 1024, 0.02, 3),              # 16 chunks of 64 columns: two per XCD
+    (900, 2500, 64, 0.01, 4),               # one chunk
+])
+def test_nzsweep_equals_fp32_csr_oracle(gpu, M, K, N, density, seed):
+    import torch
+    rowptr, colind, values = random_csr(M, K, density, seed=seed, empty_rows=0.15, heavy_rows=2,
+                                        heavy_len=K // 3)
+    B = np.random.default_rng(seed).uniform(-1, 1, (K, N)).astype(np.float32)
+    plan = _plan(rowptr, colind, values, M)
+    dB = torch.from_numpy(B).cuda()
+    want = oracle.csr_spmm_f32(rowptr, colind, values, B, M)
+    _say("nzsweep", M, K, N)
+    for W, U, D in SETTINGS:
+        got = _run(plan, dB, M, N, W, U, D)
+        assert np.array_equal(got, want), (W, U, D, float(np.nanmax(np.abs(got - want))))
+    assert_gate(gate(got, rowptr, colind, values, B, M))
+    # within fp32 rounding of the MFMA kernels' product
+    ref = plan.run(dB).cpu().numpy()
+    assert_gate(gate(ref, rowptr, colind, values, B, M))
+
+
+def test_nzsweep_uniform_pattern_deterministic(gpu):
+    """The uniform workload's shape at 1/16 scale (16 values per row at
+    distinct random columns), run twice per setting (the stream is built on
+    the first run and reused): equal to the oracle bit for bit both times."""
+    import torch
+    rng = np.random.default_rng(11)
+    M = K = 4096
+    cols = np.stack([rng.choice(K, 16, replace=False) for _ in range(M)])
+    cols.sort(axis=1)
+    rowptr = np.arange(0, 16 * M + 1, 16, dtype=np.int32)
+    colind = cols.ravel().astype(np.int32)
+    values = rng.uniform(-1, 1, colind.size).astype(np.float32)
+    B = rng.uniform(-1, 1, (K, 512)).astype(np.float32)
+    plan = _plan(rowptr, colind, values, M)
+    dB = torch.from_numpy(B).cuda()
+    want = oracle.csr_spmm_f32(rowptr, colind, values, B, M)
+    _say("nzsweep uniform-like", M)
+    for W, U, D in ((8, 32, 2), (4, 16, 2), (16, 64, 2)):
+        for _ in range(2):
+            assert np.array_equal(_run(plan, dB, M, 512, W, U, D), want), (W, U, D)
+
+
+def test_nzsweep_packed_plans_and_duplicates(gpu):
+    """Row maps (reordered packings) are applied in the store, omitted rows
+    are zeroed, and duplicated (row, col) entries follow the plan's
+    last-wins policy (the oracle runs on the deduplicated CSR)."""
+    import torch
+    M = K = 600
+    N = 128
+    rowptr, colind, values = random_csr(M, K, 0.02, seed=21, empty_rows=0.3)
+    B = np.random.default_rng(21).uniform(-1, 1, (K, N)).astype(np.float32)
+    dB = torch.from_numpy(B).cuda()
+    want = oracle.csr_spmm_f32(rowptr, colind, values, B, M)
+    for order in ("row_rcm", "jaccard_greedy", "sparse_rows"):
+        _say("nzsweep packed", order)
+        plan = _plan(rowptr, colind, values, M, row_order=order, K=K)
+        assert np.array_equal(_run(plan, dB, M, N, 8, 32, 2), want), order
+    rowptr, colind, values = random_csr(M, K, 0.02, seed=22, duplicates=True, unsorted=True)
+    drp, dci, dvv = dedupe_last(rowptr, colind, values)
+    plan = _plan(rowptr, colind, values, M)
+    _say("nzsweep duplicates")
+    assert np.array_equal(_run(plan, dB, M, N, 8, 32, 2), oracle.csr_spmm_f32(drp, dci, dvv, B, M))
+
+
+def test_nzsweep_default_knobs(gpu):
+    """grid_order 5 with every other knob 0 runs the documented defaults
+    (8 windows, sub-batches of 32, depth 2)."""
+    import torch
+    M, K, N = 500, 900, 256
+    rowptr, colind, values = random_csr(M, K, 0.02, seed=12)
+    B = np.random.default_rng(12).uniform(-1, 1, (K, N)).astype(np.float32)
+    plan = _plan(rowptr, colind, values, M)
+    dB = torch.from_numpy(B).cuda()
+    _say("nzsweep defaults", M, N)
+    want = oracle.csr_spmm_f32(rowptr, colind, values, B, M)
+    assert np.array_equal(plan.run(dB, grid_order=NZ).cpu().numpy(), want)
+    assert np.array_equal(plan.run(dB, grid_order=NZ, wg_cols=64).cpu().numpy(), want)
+
+
+def test_nzsweep_refusals_leave_c_untouched(gpu):
+    import torch
+    from mask_amd._capi import SrbcrsError
+    M, K = 300, 400
+    rowptr, colind, values = random_csr(M, K, 0.03, seed=5)
+    plan = _plan(rowptr, colind, values, M)
+    cases = [
+        (192, dict(), "divid"),                                  # 3 chunks of 64
+        (96, dict(), "multiple of 64"),
+        (128, dict(windows_per_wave=2), "windows_per_wave"),
+        (128, dict(wg_cols=128), "64 columns"),
+        (128, dict(tile_b=64, depth=4), "tile_b"),
+        (128, dict(depth=8), "tile_b, depth"),
+        (128, dict(a_operand="dense"), "compact"),
+        (128, dict(b_stage="lds"), "registers"),
+    ]
+    for N, kw, msg in cases:
+        _say("nzsweep refusal", N, kw)
+        dB = torch.ones((K, N), device="cuda")
+        out = torch.full((M, N), 7.0, device="cuda")
+        with pytest.raises(SrbcrsError, match=msg):
+            plan.run(dB, out, grid_order=NZ, **kw)
+        torch.cuda.synchronize()
+        assert bool((out == 7.0).all())
+    # misaligned B (16-byte loads)
+    big = torch.ones((K * 128 + 1,), device="cuda")
+    dB = big[1:].view(K, 128)
+    out = torch.full((M, 128), 7.0, device="cuda")
+    with pytest.raises(SrbcrsError, match="aligned"):
+        plan.run(dB, out, grid_order=NZ)
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all())
+    plan.set_schedule("split", 0)
+    out = torch.full((M, 64), 7.0, device="cuda")
+    with pytest.raises(SrbcrsError, match="row"):
+        plan.run(torch.ones((K, 64), device="cuda"), out, grid_order=NZ)
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all())
+    # 32x32 blocks have no compact copy for this kernel
+    p32 = _plan(rowptr, colind, values, M, blk_h=32, blk_w=32)
+    out = torch.full((M, 64), 7.0, device="cuda")
+    with pytest.raises(SrbcrsError, match="16x8"):
+        p32.run(torch.ones((K, 64), device="cuda"), out, grid_order=NZ)
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all())
+
+
+def test_nzsweep_many_generations(gpu):
+    """Several generations of resident waves, runs of empty groups and groups
+    of very different sizes: every row equals the oracle's fp32 product."""
+    import torch
+    rng = np.random.default_rng(3)
+    M = K = 72000
+    counts = rng.integers(0, 9, size=M)
+    counts[16 * 100:16 * 140] = 0           # 40 empty windows: whole empty groups
+    rowptr = np.zeros(M + 1, np.int64)
+    rowptr[1:] = np.cumsum(counts)
+    colind = np.concatenate([np.sort(rng.choice(K, c, replace=False)) for c in counts]).astype(np.int32)
+    values = rng.uniform(-1, 1, colind.size).astype(np.float32)
+    rowptr = rowptr.astype(np.int32)
+    N = 512
+    B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    dB = torch.from_numpy(B).cuda()
+    plan = _plan(rowptr, colind, values, M)
+    want = oracle.csr_spmm_f32(rowptr, colind, values, B, M)
+    _say("nzsweep generations", M, N)
+    for W, U, D in ((8, 32, 2), (4, 16, 4), (16, 32, 4)):
+        assert np.array_equal(_run(plan, dB, M, N, W, U, D), want), (W, U, D)
+
+
+def test_nzsweep_noalloc_needs_built_stream(gpu):
+    """srbcrs_run_noalloc refuses a nonzero-sweep setting whose stream is not
+    built (C untouched) and, once srbcrs_run_ex has built it, gives the same
+    bits."""
+    import ctypes
+    import torch
+    from mask_amd import _capi
+    L = _capi.lib()
+    M, K, N = 700, 900, 128
+    rowptr, colind, values = random_csr(M, K, 0.02, seed=31)
+    plan = _plan(rowptr, colind, values, M)
+    B = torch.from_numpy(np.random.default_rng(31).uniform(-1, 1, (K, N)).astype(np.float32)).cuda()
+    opts = _capi.RunOpts(2, 32, 0, NZ, 8, 0, 0)
+    st = torch.cuda.current_stream().cuda_stream
+
+    def call(fn, C):
+        return fn(plan.handle, B.data_ptr(), K, N, B.stride(0), C.data_ptr(), C.stride(0), M,
+                  ctypes.byref(opts), st)
+
+    _say("nzsweep noalloc")
+    got = torch.full((M, N), 7.0, device="cuda")
+    assert call(L.srbcrs_run_noalloc, got) == _capi.SRBCRS_EINVAL
+    assert "not built" in L.srbcrs_last_error().decode()
+    torch.cuda.synchronize()
+    assert bool((got == 7.0).all())
+    ref = torch.full((M, N), float("nan"), device="cuda")
+    _capi.check(call(L.srbcrs_run_ex, ref))
+    _capi.check(call(L.srbcrs_run_noalloc, got))
+    torch.cuda.synchronize()
+    assert torch.equal(got, ref)
