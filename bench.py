@@ -711,8 +711,10 @@ def algorithmic_bytes(M, N, Mo, nb, nnz, kernel, bh=16, bw=8):
 # every run times the same kernel instantiation as the committed rocprofv3 profile of that workload;
 # --tune times the candidates on the box instead.
 PUBLISHED_KNOBS = {
-    # merged windows: 4 windows' blocks interleaved per 128-column wave, column chunks pinned to XCDs
-    "uniform-65536": {"depth": 4, "wg_cols": 128, "grid_order": 4, "windows_per_wave": 4, "a_operand": "compact"},
+    # the nonzero sweep: one B-row gather per stored value, 8 windows' values per 64-column wave in the
+    # merged order, sub-batches of 32 values, 2 in flight
+    "uniform-65536": {"depth": 2, "tile_b": 32, "wg_cols": 64, "grid_order": 5, "windows_per_wave": 8,
+                      "a_operand": "compact"},
     "banded-524288": {"depth": 2, "wg_cols": 256, "grid_order": 1, "windows_per_wave": 1, "a_operand": "dense"},
     # B staged through LDS by direct-to-LDS loads
     "rmat-2^20": {"depth": 4, "wg_cols": 64, "grid_order": 3, "windows_per_wave": 1, "a_operand": "compact",
@@ -725,6 +727,7 @@ PUBLISHED_KNOBS = {
 # the HBM rate, bound by the gathers' requests out of the L2 (most served by the memory-side cache).
 BOUND = {"banded-524288": "hbm", "uniform-65536": "l2-miss gather path", "rmat-2^20": "l2-miss gather path",
          "gcn-232965": "l2-miss gather path"}
+NZSWEEP = 5   # grid order of the nonzero sweep
 # the other large configurations (banded: the second north-star target; R-MAT and the GCN
 # aggregation at N = 256), measured in the same invocation as the headline
 EXTRA_CONFIGS = ("banded-524288", "rmat-2^20", "gcn-232965")
@@ -862,7 +865,7 @@ def measure(args, config, mtx=None, cpu_seconds=None, settle_s=0.0, ceiling=None
         elif (m.name in PUBLISHED_KNOBS and N == PUBLISHED_KNOBS[m.name].get("N", 512) and args.blk == "16x8"
               and args.row_order == "identity" and not mtx):
             knob_args.update({k: v for k, v in PUBLISHED_KNOBS[m.name].items() if k != "N"})
-            knobs = {"depth": knob_args["depth"], "tile_b": 0, "wg_cols": knob_args["wg_cols"],
+            knobs = {"depth": knob_args["depth"], "tile_b": knob_args["tile_b"], "wg_cols": knob_args["wg_cols"],
                      "grid_order": knob_args["grid_order"], "windows_per_wave": knob_args["windows_per_wave"],
                      "a_operand": knob_args["a_operand"],
                      "b_stage": "lds" if knob_args["b_stage"] == "lds" else "registers", "tuned": False,
@@ -926,10 +929,12 @@ def measure(args, config, mtx=None, cpu_seconds=None, settle_s=0.0, ceiling=None
                  "grid_order": args.grid_order or 1, "windows_per_wave": args.wpw or 1,
                  "a_operand": a_operand_used(plan, args.a_operand),
                  "b_stage": "lds" if args.b_stage == "lds" else "registers", "tuned": False}
-    ab = algorithmic_bytes(m.M, N, Mo, nb, m.nnz, args.kernel, bh, bw)
-    compulsory = (nb * (bw * 4 + bh * bw * 4) + 4 * (Mo + 1) if args.kernel == "srbcrs" else 8 * m.nnz) \
-        + m.K * N * 4 + m.M * N * 4
-    padded_flops = 2.0 * bh * bw * nb * N
+    # the nonzero sweep reads (column, value) pairs and gathers one B row per value, as CSR does, and
+    # does no MFMA work; the MFMA kernels read the blocks and gather BW rows per block
+    vector = args.kernel == "csr" or knob_args.get("grid_order") == NZSWEEP
+    ab = algorithmic_bytes(m.M, N, Mo, nb, m.nnz, "csr" if vector else "srbcrs", bh, bw)
+    compulsory = (8 * m.nnz if vector else nb * (bw * 4 + bh * bw * 4) + 4 * (Mo + 1)) + m.K * N * 4 + m.M * N * 4
+    padded_flops = 0.0 if vector else 2.0 * bh * bw * nb * N
     prof = None
     if args.kernel == "srbcrs" and args.schedule == "auto" and not args.tile_b and args.row_order == "identity" \
             and not mtx:
@@ -1073,6 +1078,7 @@ def measured_profile(workload, N, kernel, knobs, blk="16x8"):
     if kernel != "srbcrs" or knobs is None:
         return None
     want = {k: str(knobs[k]) for k in ("depth", "wg_cols", "grid_order", "windows_per_wave", "a_operand")}
+    want["tile_b"] = str(knobs.get("tile_b", 0) or 0)
     want["blk"] = blk
     want["b_stage"] = str(knobs.get("b_stage", "registers"))
     for path in sorted((ROOT / "profiles").glob(f"spmm_*_{workload.replace('^', '')}_N{N}*.md")):
@@ -1085,7 +1091,8 @@ def measured_profile(workload, N, kernel, knobs, blk="16x8"):
                 fields["kernel_avg_ms"] = round(int(val) / 1e6, 5)
             elif key == "knobs":
                 prof_knobs = dict(kv.split("=") for kv in val.split())
-        if prof_knobs and {"windows_per_wave": "1", "blk": "16x8", "b_stage": "registers", **prof_knobs} == want \
+        if prof_knobs and {"windows_per_wave": "1", "blk": "16x8", "b_stage": "registers", "tile_b": "0",
+                           **prof_knobs} == want \
                 and "l2_egress_bytes" in fields:
             return {"file": f"profiles/{path.name}", "traffic_bytes": fields.get("traffic_bytes"), **fields}
     return None

@@ -257,7 +257,7 @@ int srbcrs_plan_trim(srbcrs_plan *plan, void *stream);
  *                indices and A words on the host (it allocates),
  *                5 = nonzero sweep: the vector kernel for low block density
  *                ("row" schedule, 16x8 blocks with the compact A copy).
- *                One wave per windows_per_wave windows (4, 8 or 16; 0 = 8)
+ *                One wave per windows_per_wave windows (4 or 8; 0 = 8)
  *                and 64 columns walks the windows' stored values in the
  *                merged order (one 256-byte B-row gather and one LDS
  *                read-add-write per value, no padded block arithmetic);
@@ -267,7 +267,7 @@ int srbcrs_plan_trim(srbcrs_plan *plan, void *stream);
  *                multiple of 64 with N / 64 dividing 8 or a multiple of 8,
  *                ldb and ldc multiples of 4, 16-byte aligned B and C,
  *                K * ldb * 4 < 2^32, ldb * 4 < 2^24 and column indices
- *                below 2^23.  C[r, :] is the sum of fl(v * B[c, :]) over
+ *                below 2^24.  C[r, :] is the sum of fl(v * B[c, :]) over
  *                the row's stored values in ascending column order, each
  *                product rounded before it is added (the fp32 CSR product,
  *                not the MFMA kernels' bits).  The first run per setting

@@ -458,7 +458,7 @@ struct srbcrs_plan {
   // sub-batch size U and chunk size (key nz_key)
   struct Nz {
     int32_t* d_eoff = nullptr;   // group g's pairs: [eoff[g], eoff[g+1])
-    uint2* d_pairs = nullptr;    // ((B row << 9) | tile row, value bits)
+    uint2* d_pairs = nullptr;    // ((tile row << 24) | B row, value bits)
     int64_t entries = 0;
   };
   std::map<int64_t, Nz> nz;
@@ -760,13 +760,13 @@ const srbcrs_plan::Nz& nz_stream(srbcrs_plan& plan, int W, int U, int D, hipStre
   if (it != plan.nz.end()) return it->second;
   const int kChunk = 2 * D * U;      // the kernel's loop body
   const int E = 4, Q = U / E;   // entries per gather instruction, instructions per sub-batch
-  constexpr int kRowBits = 9;
+  constexpr int kRowShift = 24;   // entry = (tile row << 24) | B row
   constexpr int kWords = 16 * 8 / 32;
   const int64_t nb = plan.total;
   const int Mo = plan.Mo;
-  if (plan.max_col >= (1 << (32 - kRowBits)))
+  if (plan.max_col >= (1 << kRowShift))
     fail(SRBCRS_EINVAL, "the nonzero sweep takes B-row indices below 2^%d (the matrix references column %d)",
-         32 - kRowBits, plan.max_col);
+         kRowShift, plan.max_col);
   std::vector<int32_t> sidx((size_t)nb * 8);
   std::vector<uint2> words((size_t)nb * kWords);
   std::vector<float> packed((size_t)plan.n_apacked);
@@ -807,7 +807,7 @@ const srbcrs_plan::Nz& nz_stream(srbcrs_plan& plan, int W, int U, int D, hipStre
               const uint2 wd = words[(size_t)b * kWords + (pos >> 5)];
               const int bit = pos & 31;
               if (!((wd.x >> bit) & 1u)) continue;
-              le.push_back(((uint32_t)sidx[(size_t)b * 8 + k] << kRowBits) | (uint32_t)(16 * w + row));
+              le.push_back(((uint32_t)(16 * w + row) << kRowShift) | (uint32_t)sidx[(size_t)b * 8 + k]);
               lv.push_back(packed[(size_t)wd.y + __builtin_popcount(wd.x & ((1u << bit) - 1u))]);
             }
         }
@@ -818,16 +818,17 @@ const srbcrs_plan::Nz& nz_stream(srbcrs_plan& plan, int W, int U, int D, hipStre
       const size_t n = le.size();
       taken.assign(n, 0);
       size_t head = 0;
-      uint32_t prev = le.empty() ? 0u : le[0] >> kRowBits;
+      const uint32_t kBRow = (1u << kRowShift) - 1u;
+      uint32_t prev = le.empty() ? 0u : le[0] & kBRow;
       auto put = [&](int u, uint32_t e, float v) {
         batch[(size_t)((u % E) * Q + u / E)] = uint2{e, __builtin_bit_cast(uint32_t, v)};
       };
       while (head < n) {
-        uint64_t used[8] = {0, 0, 0, 0, 0, 0, 0, 0}, held[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        uint64_t used[4] = {0, 0, 0, 0}, held[4] = {0, 0, 0, 0};
         int got = 0;
         for (size_t i = head; i < n && i < head + 4 * (size_t)U && got < U; ++i) {
           if (taken[i]) continue;
-          const uint32_t t = le[i] & ((1u << kRowBits) - 1u);
+          const uint32_t t = le[i] >> kRowShift;
           const uint64_t bit = 1ull << (t & 63);
           if ((used[t >> 6] | held[t >> 6]) & bit) {
             held[t >> 6] |= bit;
@@ -836,14 +837,14 @@ const srbcrs_plan::Nz& nz_stream(srbcrs_plan& plan, int W, int U, int D, hipStre
           used[t >> 6] |= bit;
           taken[i] = 1;
           put(got, le[i], lv[i]);
-          prev = le[i] >> kRowBits;
+          prev = le[i] & kBRow;
           ++got;
         }
-        for (; got < U; ++got) put(got, (prev << kRowBits) | dummy, 0.f);
+        for (; got < U; ++got) put(got, (dummy << kRowShift) | prev, 0.f);
         op.insert(op.end(), batch.begin(), batch.end());
         while (head < n && taken[head]) ++head;
       }
-      while (op.size() % kChunk) op.push_back(uint2{(prev << kRowBits) | dummy, 0u});
+      while (op.size() % kChunk) op.push_back(uint2{(dummy << kRowShift) | prev, 0u});
     }
   });
   std::vector<int32_t> eoff((size_t)n_groups + 1, 0);
@@ -1372,8 +1373,8 @@ static void run_impl(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
       if (opts->wg_cols && opts->wg_cols != 64)
         fail(SRBCRS_EINVAL, "the nonzero sweep runs 64 columns per wave (got wg_cols %d)", opts->wg_cols);
       if (!srbcrs::nz_setting_ok(W, U, D))
-        fail(SRBCRS_EINVAL, "the nonzero sweep takes windows_per_wave 4, 8 or 16 and (tile_b, depth) (16, 2), (16, 4) "
-                            "or (32, 2) (got %d, %d, %d)", W, U, D);
+        fail(SRBCRS_EINVAL, "the nonzero sweep takes windows_per_wave 4 or 8 and (tile_b, depth) (16, 2), (16, 4), "
+                            "(32, 2), (32, 4) or (64, 2) (got %d, %d, %d)", W, U, D);
       if (N % 64 || !srbcrs::merged_chunks_ok((int)(N / 64)))
         fail(SRBCRS_EINVAL, "the nonzero sweep needs N a multiple of 64 with N / 64 column chunks dividing 8 or a "
                             "multiple of 8");

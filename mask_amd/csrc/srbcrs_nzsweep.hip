@@ -7,10 +7,11 @@
 
 namespace srbcrs {
 
-// W 4, 8 or 16 windows per group; U entries per sub-batch and D sub-batches in
+// W 4 or 8 windows per group (tile rows and the padding row fit the entry's
+// top byte); U entries per sub-batch and D sub-batches in
 // the gather ring: (16, 2), (16, 4), (32, 2), (32, 4) or (64, 2).
 bool nz_setting_ok(int W, int U, int D) {
-  if (W != 4 && W != 8 && W != 16) return false;
+  if (W != 4 && W != 8) return false;
   return (U == 16 && (D == 2 || D == 4)) || (U == 32 && (D == 2 || D == 4)) || (U == 64 && D == 2);
 }
 
@@ -35,7 +36,6 @@ static hipError_t launch_nz_w(const NzArgs& z, const StreamArgs& a, int U, int D
 
 hipError_t launch_nzsweep(const NzArgs& z, const StreamArgs& a, int U, int D, hipStream_t st) {
   if (!nz_setting_ok(z.W, U, D) || a.N % 64 != 0) return hipErrorInvalidValue;
-  if (z.W == 16) return launch_nz_w<16>(z, a, U, D, st);
   return z.W == 8 ? launch_nz_w<8>(z, a, U, D, st) : launch_nz_w<4>(z, a, U, D, st);
 }
 

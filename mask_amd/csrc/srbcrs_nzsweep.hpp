@@ -15,7 +15,7 @@
 //
 // Stream (built on the host per plan and setting, srbcrs_capi.cpp): group
 // g's entries [eoff[g], eoff[g+1]), each an (entry, value) pair, entry =
-// (B row << 9) | tile row, tile row = 16 * (window - g*W) + row in the
+// (tile row << 24) | B row, tile row = 16 * (window - g*W) + row in the
 // window.  Within a group the values follow the merged unit order (block r
 // of every window, in window order, then block r + 1), within a block
 // column by column, cut into sub-batches of distinct tile rows; padding
@@ -34,7 +34,7 @@
 
 namespace srbcrs {
 
-constexpr int kNzRowBits = 9;   // tile-row field of an entry (16*W + 1 <= 512)
+constexpr int kNzRowShift = 24;   // entry = (tile row << 24) | B row: 16*W + 1 <= 256, B rows < 2^24
 
 // Each step's loads are pinned ahead of its adds (sched_barrier): left to
 // itself the compiler hoisted the multiplies above the next sub-batch's
@@ -46,28 +46,31 @@ constexpr int kNzRowBits = 9;   // tile-row field of an entry (16*W + 1 <= 512)
 #endif
 
 // Lane l of a wave64 broadcast to the 16 lanes of its row (DPP
-// row_newbcast), l = 16 * row + q.
+// row_newbcast), l = 16 * row + q.  Every lane of a row reads a valid
+// source lane, so no old value is needed (mov_dpp, bound_ctrl).
+#define SRBCRS_ROW_BCAST(q) return (uint32_t)__builtin_amdgcn_mov_dpp(x, 0x150 + (q), 0xf, 0xf, true)
 __device__ __forceinline__ uint32_t row_bcast(uint32_t v, int q) {
   const int x = (int)v;
   switch (q) {
-    case 0: return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x150, 0xf, 0xf, false);
-    case 1: return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x151, 0xf, 0xf, false);
-    case 2: return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x152, 0xf, 0xf, false);
-    case 3: return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x153, 0xf, 0xf, false);
-    case 4: return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x154, 0xf, 0xf, false);
-    case 5: return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x155, 0xf, 0xf, false);
-    case 6: return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x156, 0xf, 0xf, false);
-    case 7: return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x157, 0xf, 0xf, false);
-    case 8: return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x158, 0xf, 0xf, false);
-    case 9: return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x159, 0xf, 0xf, false);
-    case 10: return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x15a, 0xf, 0xf, false);
-    case 11: return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x15b, 0xf, 0xf, false);
-    case 12: return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x15c, 0xf, 0xf, false);
-    case 13: return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x15d, 0xf, 0xf, false);
-    case 14: return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x15e, 0xf, 0xf, false);
-    default: return (uint32_t)__builtin_amdgcn_update_dpp(0, x, 0x15f, 0xf, 0xf, false);
+    case 0: SRBCRS_ROW_BCAST(0);
+    case 1: SRBCRS_ROW_BCAST(1);
+    case 2: SRBCRS_ROW_BCAST(2);
+    case 3: SRBCRS_ROW_BCAST(3);
+    case 4: SRBCRS_ROW_BCAST(4);
+    case 5: SRBCRS_ROW_BCAST(5);
+    case 6: SRBCRS_ROW_BCAST(6);
+    case 7: SRBCRS_ROW_BCAST(7);
+    case 8: SRBCRS_ROW_BCAST(8);
+    case 9: SRBCRS_ROW_BCAST(9);
+    case 10: SRBCRS_ROW_BCAST(10);
+    case 11: SRBCRS_ROW_BCAST(11);
+    case 12: SRBCRS_ROW_BCAST(12);
+    case 13: SRBCRS_ROW_BCAST(13);
+    case 14: SRBCRS_ROW_BCAST(14);
+    default: SRBCRS_ROW_BCAST(15);
   }
 }
+#undef SRBCRS_ROW_BCAST
 
 // 64 columns per wave, W windows per group, sub-batches of U entries.  One
 // gather instruction serves 4 entries: lane (g, i) = (lane / 16, lane % 16)
@@ -86,7 +89,10 @@ __device__ __forceinline__ uint32_t row_bcast(uint32_t v, int q) {
 // last (their loads are never added), so every step issues the same loads
 // and the compiler's vmcnt waits count them exactly.  B + col0 is addressed
 // through a buffer resource with 32-bit offsets: K * ldb * 4 < 2^32, and B
-// rows and ldb * 4 below 2^24 (24-bit multiplies).
+// rows and ldb * 4 below 2^24 (24-bit multiplies).  Per gather instruction
+// the lane needs two addresses from its entry: the B offset, one 24-bit
+// multiply-add of the entry's low 24 bits, and the LDS byte offset (tile row
+// << 8) | (16 * i), one byte permute of the entry's high byte.
 template <int W, int U, int D>
 __global__ __launch_bounds__(64) void spmm_nzsweep(const int* __restrict__ eoff, const uint2* __restrict__ pairs,
                                                    const float* __restrict__ B, float* __restrict__ C,
@@ -95,9 +101,8 @@ __global__ __launch_bounds__(64) void spmm_nzsweep(const int* __restrict__ eoff,
   constexpr int ROWS = 16 * W;
   constexpr int Q = U / 4;   // gather instructions per sub-batch
   constexpr int P = 2 * D;   // steps per loop body
-  static_assert(ROWS + 1 <= (1 << kNzRowBits), "tile rows fit the entry's row field");
+  static_assert(ROWS + 1 <= (1 << (32 - kNzRowShift)), "tile rows fit the entry's row byte");
   static_assert(U % 4 == 0 && Q <= 16 && D >= 2, "a sub-batch's pairs fit one load per lane");
-  constexpr uint32_t kRowMask = (1u << kNzRowBits) - 1u;
   __shared__ __attribute__((aligned(16))) float tile[(ROWS + 1) * 64];
   int64_t g;
   int c;
@@ -119,15 +124,19 @@ __global__ __launch_bounds__(64) void spmm_nzsweep(const int* __restrict__ eoff,
     const uint32_t boff = (uint32_t)sub * 16u;
     const int64_t n_sb = (e1 - e0) / U;
     const uint2* gp = pairs + e0 + grp * Q + (sub % Q);
+    char* tileb = reinterpret_cast<char*>(tile);
     uint2 m[P];
     f4 b[D][Q];
+    uint32_t la[D][Q];   // LDS byte offsets of the gathered rows' tile rows
     auto fetch = [&](int ms, int64_t j) { m[ms] = gp[(j < n_sb ? j : n_sb - 1) * U]; };
     auto issue = [&](int bs, int ms) {
 #pragma unroll
       for (int q = 0; q < Q; ++q) {
         const uint32_t w = row_bcast(m[ms].x, q);
-        b[bs][q] = __builtin_bit_cast(
-            f4, __builtin_amdgcn_raw_buffer_load_b128(rs, __umul24(w >> kNzRowBits, ldb4) + boff, 0, 0));
+        // byte 0 = 16 i, byte 1 = the entry's top byte (the tile row)
+        la[bs][q] = __builtin_amdgcn_perm(w, boff, 0x0c0c0700u);
+        b[bs][q] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(
+                                              rs, __umul24(w, ldb4) + boff, 0, 0));   // the low 24 bits: the B row
       }
     };
     // tile rows of one sub-batch are distinct (the dummy row aside), so its
@@ -137,27 +146,27 @@ __global__ __launch_bounds__(64) void spmm_nzsweep(const int* __restrict__ eoff,
     // and complete while the step issues its loads and waits for its
     // gathers.  (LDS float atomics, ds_add_f32, ran the same work about ten
     // times slower.)
-    int t[Q];
     f4 o[Q];
-    auto read = [&](int ms) {
+    auto read = [&](int bs) {
 #pragma unroll
-      for (int q = 0; q < Q; ++q) {
-        t[q] = (int)(row_bcast(m[ms].x, q) & kRowMask) * 16 + sub;
-        o[q] = tile4[t[q]];
-      }
+      for (int q = 0; q < Q; ++q) o[q] = *reinterpret_cast<const f4*>(tileb + la[bs][q]);
     };
     auto add = [&](int bs, int ms) {
 #pragma clang fp contract(off)
 #pragma unroll
       for (int q = 0; q < Q; ++q) {
         const f4 p = __builtin_bit_cast(float, row_bcast(m[ms].y, q)) * b[bs][q];
-        tile4[t[q]] = o[q] + p;
+        *reinterpret_cast<f4*>(tileb + la[bs][q]) = o[q] + p;
       }
     };
+    // the prologue in steady-state order (pairs, then gathers), pinned: the
+    // loop's first wait then counts the same loads on both incoming paths
 #pragma unroll
     for (int j = 0; j < D; ++j) fetch(j, j);
+    SRBCRS_NZ_PIN;
 #pragma unroll
     for (int j = 0; j + 1 < D; ++j) issue(j, j);
+    SRBCRS_NZ_PIN;
     read(0);
     for (int64_t base = 0; base < n_sb; base += P) {
 #pragma unroll
@@ -166,7 +175,7 @@ __global__ __launch_bounds__(64) void spmm_nzsweep(const int* __restrict__ eoff,
         issue((k + D - 1) % D, (k + D - 1) % P);
         SRBCRS_NZ_PIN;
         add(k % D, k % P);
-        read((k + 1) % P);
+        read((k + 1) % D);
         SRBCRS_NZ_PIN;
       }
     }
