@@ -529,7 +529,8 @@ def test_committed_profiles_are_physical():
                 assert gbs <= bench.HBM_PEAK_GBS, (path.name, key, gbs)
     assert found >= 1
     for name, knobs in bench.PUBLISHED_KNOBS.items():
-        k = dict({key: v for key, v in knobs.items() if key != "N"}, tile_b=0)
+        k = dict({key: v for key, v in knobs.items() if key != "N"})
+        k.setdefault("tile_b", 0)
         k.setdefault("b_stage", "registers")
         prof = bench.measured_profile(name, knobs.get("N", 512), "srbcrs", k)
         assert prof is not None and prof["l2_egress_bytes"] > 0, name
