@@ -744,16 +744,17 @@ int64_t nz_key(int W, int U, int D) { return ((int64_t)W << 16) | ((int64_t)U <<
 // sub-batches of U entries (spmm_nzsweep, srbcrs_nzsweep.hpp).  A group's
 // stored values are listed in the merged unit order (block r of each window
 // in window order, then r + 1), within a block column by column and, in a
-// column, row by row; each is the entry (B row << 8) | (16 * window slot +
-// row) with its value.  The list is then cut into sub-batches of U entries
+// column, row by row; each is the entry ((16 * window slot + row) << 24) |
+// B row with its value.  The list is then cut into sub-batches of U entries
 // with distinct tile rows: each sub-batch takes, in list order, the entries
 // among the next 4U not yet taken whose row is neither in the sub-batch nor
 // held by an earlier entry left behind, so every row keeps its values in
 // list order (ascending columns); a sub-batch short of U is filled with
 // entries for tile row 16 * W (never stored) that repeat the previous B row
-// (a cache hit).  Groups are padded the same way to whole chunks (of
-// max(64, U * D) entries: the kernel reads a chunk's entries ahead).
-// Built on the host from the plan's sidx, compact A words and packed values.
+// (a cache hit).  Groups are padded the same way to whole loop bodies of
+// the kernel (2D sub-batches).  Each sub-batch is stored transposed for the
+// kernel's gather instructions (pair g * U/4 + q = entry 4q + g).  Built on
+// the host from the plan's sidx, compact A words and packed values.
 const srbcrs_plan::Nz& nz_stream(srbcrs_plan& plan, int W, int U, int D, hipStream_t st) {
   const int64_t key = nz_key(W, U, D);
   auto it = plan.nz.find(key);
