@@ -679,7 +679,7 @@ def gcn_train_bench(args):
 
 
 def tuned_knobs(t, tune_s):
-    return {"depth": t["depth"], "tile_b": 0, "wg_cols": t["wg_cols"], "grid_order": t["grid_order"],
+    return {"depth": t["depth"], "tile_b": t.get("tile_b", 0), "wg_cols": t["wg_cols"], "grid_order": t["grid_order"],
             "windows_per_wave": t["windows_per_wave"], "a_operand": t["a_operand"], "b_stage": t["b_stage"],
             "tuned": True,
             "tune_s": round(tune_s, 3)}
@@ -858,7 +858,7 @@ def measure(args, config, mtx=None, cpu_seconds=None, settle_s=0.0, ceiling=None
     if args.kernel == "srbcrs" and not explicit_knobs(args):
         if args.tune:
             t0 = time.time()
-            tuned = plan.tune(B, C)   # outside the timed region, like the conversion
+            tuned = plan.tune(B, C, nonzero_sweep=True)   # outside the timed region, like the conversion
             torch.cuda.synchronize()
             tune_s = time.time() - t0
             knobs = tuned_knobs(tuned, tune_s)
@@ -988,14 +988,16 @@ def measure(args, config, mtx=None, cpu_seconds=None, settle_s=0.0, ceiling=None
 
     if knobs.get("source") == "bench.PUBLISHED_KNOBS" and not args.lean:
         # beside the published setting: what the library picks for itself on
-        # this plan (srbcrs_plan_tune, the drop-in's autotune), timed the same way
+        # this plan (srbcrs_plan_tune_ex with the nonzero sweep admitted: the
+        # drop-in's autotune under SPARSENE_ALLOW_CSR_FALLBACK=1), timed the same way
         t0 = time.time()
-        tk = plan.tune(B, C)
+        tk = plan.tune(B, C, nonzero_sweep=True)
         torch.cuda.synchronize()
         tune_s = time.time() - t0
         ms_t = _time_ms(lambda: plan.run(B, C), args.steps, args.warmup)
         same = all(str(tk[k]) == str(knobs[k]) for k in ("depth", "wg_cols", "grid_order", "windows_per_wave",
-                                                          "a_operand", "b_stage"))
+                                                          "a_operand", "b_stage")) \
+            and (tk["grid_order"] != NZSWEEP or tk["tile_b"] == knobs.get("tile_b"))
         result["library_tuned"] = {"knobs": tk, "tune_s": round(tune_s, 3), "ms_per_step": round(ms_t, 5),
                                    "value": round(flops / (ms_t / 1e3) / 1e9, 2), "same_as_published": same}
 

@@ -360,12 +360,26 @@ size_t srbcrs_noalloc_scratch_floats(void);
  * srbcrs_run calls, and srbcrs_run_ex calls whose knobs are all 0, use it
  * at that N until the schedule changes.  C is overwritten (with the
  * product).  Every candidate gives the same bits: tuning changes only the
- * time.  best (may be NULL) receives the choice.  Not thread-safe against a
+ * time (srbcrs_plan_tune_ex can add candidates that do not).  best (may be NULL) receives the choice.  Not thread-safe against a
  * concurrent srbcrs_run* on the same plan.  No reference counterpart: the
  * reference fixes its launch shape offline (strategy_agent.py:81-130). */
 int srbcrs_plan_tune(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int64_t ldb,
                      float *d_C, int64_t ldc, int64_t c_rows, int32_t reps, srbcrs_run_opts *best,
                      void *stream);
+
+/* srbcrs_plan_tune with flags (srbcrs_plan_tune = flags 0).
+ * SRBCRS_TUNE_NONZERO_SWEEP adds, last, the nonzero sweep (grid order 5;
+ * "row" schedule, 16x8 blocks with the compact copy) at (windows_per_wave,
+ * tile_b, depth) = (8, 32, 2), (4, 16, 2), (4, 16, 4), (8, 32, 4): a choice
+ * among them gives the fp32 CSR product's bits instead of the MFMA
+ * kernels' (equal within fp32 rounding), the caller's opt-in, as the
+ * reference's SPARSENE_ALLOW_CSR_FALLBACK is (external_backend_spmm.py:40-95).
+ * Each stream a candidate needs is built on the host at its first run.
+ * Other flag bits are rejected.  No reference counterpart. */
+#define SRBCRS_TUNE_NONZERO_SWEEP 1
+int srbcrs_plan_tune_ex(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int64_t ldb,
+                        float *d_C, int64_t ldc, int64_t c_rows, int32_t reps, int32_t flags,
+                        srbcrs_run_opts *best, void *stream);
 
 /* ---- Sharding over GPUs (design support; this build runs on one GPU).
  * Cut the row windows into n_shards contiguous ranges of near-equal cost

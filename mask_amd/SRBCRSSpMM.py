@@ -162,21 +162,24 @@ class Plan:
                                                   int(out.shape[0]), ctypes.byref(opts), _stream_handle(self.device)))
         return out
 
-    def tune(self, dense: Tensor, out: Optional[Tensor] = None, reps: int = 3) -> dict:
+    def tune(self, dense: Tensor, out: Optional[Tensor] = None, reps: int = 3, nonzero_sweep: bool = False) -> dict:
         """Time the launch candidates for dense.shape[1] on this plan (see
         srbcrs_plan_tune) and keep the fastest for later default-knob runs
         at that width; returns the choice.  out (or a scratch tensor) is
-        overwritten with A @ dense."""
+        overwritten with A @ dense.  nonzero_sweep=True also times the
+        nonzero sweep (srbcrs_plan_tune_ex, SRBCRS_TUNE_NONZERO_SWEEP),
+        whose bits are the fp32 CSR product's."""
         out = self._operands(dense, out)
         best = _capi.RunOpts()
+        flags = _capi.SRBCRS_TUNE_NONZERO_SWEEP if nonzero_sweep else 0
         with torch.cuda.device(self.device):
-            _capi.check(_capi.lib().srbcrs_plan_tune(self._h, dense.data_ptr(), int(dense.shape[0]),
-                                                     int(dense.shape[1]), int(dense.stride(0)), out.data_ptr(),
-                                                     int(out.stride(0)), int(out.shape[0]), int(reps),
-                                                     ctypes.byref(best), _stream_handle(self.device)))
+            _capi.check(_capi.lib().srbcrs_plan_tune_ex(self._h, dense.data_ptr(), int(dense.shape[0]),
+                                                        int(dense.shape[1]), int(dense.stride(0)), out.data_ptr(),
+                                                        int(out.stride(0)), int(out.shape[0]), int(reps), flags,
+                                                        ctypes.byref(best), _stream_handle(self.device)))
         self.tuned_widths.add(int(dense.shape[1]))
         inv = {v: k for k, v in _capi.A_OPERANDS.items()}
-        return {"depth": best.depth, "wg_cols": best.wg_cols, "grid_order": best.grid_order,
+        return {"depth": best.depth, "tile_b": best.tile_b, "wg_cols": best.wg_cols, "grid_order": best.grid_order,
                 "windows_per_wave": best.windows_per_wave or 1, "a_operand": inv[best.a_operand],
                 "b_stage": "lds" if best.b_stage == 2 else "registers"}
 
@@ -363,7 +366,10 @@ def _run(dense: Tensor, row_window_offset: Tensor, tcblocktile_id: Tensor, tcblo
     plan.set_schedule(*(sched or ("auto", 0)))
     out = torch.empty((entry.num_nodes, n), dtype=torch.float32, device=dense.device)
     if os.environ.get("SPARSENE_SRBCRS_AUTOTUNE", "0") == "1" and n not in plan.tuned_widths:
-        plan.tune(dense, out)   # once per (width, schedule); the product lands in out
+        # once per (width, schedule); the product lands in out.  With the
+        # reference's CSR-fallback opt-in the nonzero sweep (the CSR
+        # product's bits) competes too.
+        plan.tune(dense, out, nonzero_sweep=os.environ.get("SPARSENE_ALLOW_CSR_FALLBACK", "0") == "1")
     else:
         plan.run(dense, out)
     return [out]

@@ -27,6 +27,7 @@ SRBCRS_EINVAL = -1
 SRBCRS_EHIP = -2
 SRBCRS_ENOMEM = -3
 SRBCRS_ESTATE = -4
+SRBCRS_TUNE_NONZERO_SWEEP = 1
 
 # Every symbol include/srbcrs.h declares (checked by the CPU test suite).
 EXPORTS = (
@@ -37,7 +38,7 @@ EXPORTS = (
     "srbcrs_schedule_build", "srbcrs_schedule_info", "srbcrs_schedule_export", "srbcrs_schedule_destroy",
     "srbcrs_plan_set_schedule", "srbcrs_run", "srbcrs_run_ex", "srbcrs_csr_spmm",
     "srbcrs_row_order", "srbcrs_pack_count", "srbcrs_pack_fill", "srbcrs_plan_create_ex", "srbcrs_plan_row_order",
-    "srbcrs_plan_tune", "srbcrs_shard_windows", "srbcrs_run_noalloc", "srbcrs_noalloc_scratch_floats",
+    "srbcrs_plan_tune", "srbcrs_plan_tune_ex", "srbcrs_shard_windows", "srbcrs_run_noalloc", "srbcrs_noalloc_scratch_floats",
     "srbcrs_plan_trim",
 )
 
@@ -143,6 +144,8 @@ def lib() -> ctypes.CDLL:
         "srbcrs_shard_windows": ([_vp, _i32, _i32, _vp], ctypes.c_int),
         "srbcrs_plan_tune": ([_vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i32, ctypes.POINTER(RunOpts), _vp],
                              ctypes.c_int),
+        "srbcrs_plan_tune_ex": ([_vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i32, _i32, ctypes.POINTER(RunOpts),
+                                 _vp], ctypes.c_int),
         "srbcrs_csr_spmm": ([_vp, _vp, _vp, _i32, _i64, _i32, _vp, _i64, _i64, _i64, _vp, _i64, _vp],
                             ctypes.c_int),
         "srbcrs_run_noalloc": ([_vp, _vp, _i64, _i64, _i64, _vp, _i64, _i64, ctypes.POINTER(RunOpts), _vp],

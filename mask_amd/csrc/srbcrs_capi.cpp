@@ -1541,8 +1541,16 @@ int srbcrs_gather_probe(const int32_t* d_rows, const int64_t* d_row_off, int32_t
 
 int srbcrs_plan_tune(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int64_t ldb, float* d_C,
                      int64_t ldc, int64_t c_rows, int32_t reps, srbcrs_run_opts* best, void* stream) {
+  return srbcrs_plan_tune_ex(plan, d_B, K, N, ldb, d_C, ldc, c_rows, reps, 0, best, stream);
+}
+
+int srbcrs_plan_tune_ex(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, int64_t ldb, float* d_C,
+                        int64_t ldc, int64_t c_rows, int32_t reps, int32_t flags, srbcrs_run_opts* best,
+                        void* stream) {
   if (!plan) return guarded([] { fail(SRBCRS_EINVAL, "plan is NULL"); });
   if (reps < 1 || reps > 100) return guarded([&] { fail(SRBCRS_EINVAL, "reps must be in [1, 100] (got %d)", reps); });
+  if (flags & ~SRBCRS_TUNE_NONZERO_SWEEP)
+    return guarded([&] { fail(SRBCRS_EINVAL, "unknown tune flags 0x%x", (unsigned)flags); });
   hipStream_t st = static_cast<hipStream_t>(stream);
   plan->tuned.erase(N);
   std::vector<srbcrs_run_opts> cand, merged_cand;
@@ -1610,8 +1618,22 @@ int srbcrs_plan_tune(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
             cand.push_back(o);
           }
   }
-  // merged-window candidates last (a near-tie keeps the plainer setting); one
-  // the operands cannot run (B / C alignment, ldb / ldc) is dropped here
+  if ((flags & SRBCRS_TUNE_NONZERO_SWEEP) && plan->sched.policy == "row" && plan->blk_h == 16 && plan->d_awords)
+    // the nonzero sweep (its bits are the fp32 CSR product's): (windows, values
+    // per sub-batch, sub-batches in flight)
+    for (const auto& nz : {std::array<int32_t, 3>{8, 32, 2}, std::array<int32_t, 3>{4, 16, 2},
+                           std::array<int32_t, 3>{4, 16, 4}, std::array<int32_t, 3>{8, 32, 4}}) {
+      srbcrs_run_opts o{};
+      o.windows_per_wave = nz[0];
+      o.tile_b = nz[1];
+      o.depth = nz[2];
+      o.grid_order = SRBCRS_GRID_NZSWEEP;
+      o.a_operand = SRBCRS_A_COMPACT;
+      merged_cand.push_back(o);
+    }
+  // merged-window and nonzero-sweep candidates last (a near-tie keeps the
+  // plainer setting); one the operands cannot run (N, B / C alignment, ldb /
+  // ldc, B's extent) is dropped here
   const size_t n_plain = cand.size();
   cand.insert(cand.end(), merged_cand.begin(), merged_cand.end());
   hipEvent_t e0 = nullptr, e1 = nullptr;
@@ -1622,7 +1644,7 @@ int srbcrs_plan_tune(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
   std::vector<float> ms_of(cand.size(), -1.f);
   for (size_t i = 0; rc == SRBCRS_OK && i < cand.size(); ++i) {
     rc = srbcrs_run_ex(plan, d_B, K, N, ldb, d_C, ldc, c_rows, &cand[i], stream);   // warm-up, validates
-    if (rc == SRBCRS_EINVAL && i >= n_plain) {   // a merged setting these operands cannot run
+    if (rc == SRBCRS_EINVAL && i >= n_plain) {   // a merged / sweep setting these operands cannot run
       rc = SRBCRS_OK;
       continue;
     }

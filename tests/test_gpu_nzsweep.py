@@ -221,3 +221,32 @@ def test_nzsweep_noalloc_needs_built_stream(gpu):
     _capi.check(call(L.srbcrs_run_noalloc, got))
     torch.cuda.synchronize()
     assert torch.equal(got, ref)
+
+
+def test_tune_ex_admits_the_sweep(gpu):
+    """srbcrs_plan_tune_ex with SRBCRS_TUNE_NONZERO_SWEEP keeps a setting
+    whose later default-knob runs give its own bits (the fp32 CSR product's
+    when it picked the sweep, the MFMA kernels' otherwise); unknown flag
+    bits are refused."""
+    import ctypes
+    import torch
+    from mask_amd import _capi
+    rng = np.random.default_rng(41)
+    M = K = 8192
+    cols = np.stack([np.sort(rng.choice(K, 16, replace=False)) for _ in range(M)])
+    rowptr = np.arange(0, 16 * M + 1, 16, dtype=np.int32)
+    colind = cols.ravel().astype(np.int32)
+    values = rng.uniform(-1, 1, colind.size).astype(np.float32)
+    B = rng.uniform(-1, 1, (K, 512)).astype(np.float32)
+    plan = _plan(rowptr, colind, values, M)
+    dB = torch.from_numpy(B).cuda()
+    mfma = plan.run(dB).cpu().numpy()
+    csr = oracle.csr_spmm_f32(rowptr, colind, values, B, M)
+    _say("tune_ex")
+    choice = plan.tune(dB, reps=2, nonzero_sweep=True)
+    got = plan.run(dB).cpu().numpy()
+    assert np.array_equal(got, csr if choice["grid_order"] == NZ else mfma), choice
+    out = torch.empty((M, 512), device="cuda")
+    rc = _capi.lib().srbcrs_plan_tune_ex(plan.handle, dB.data_ptr(), K, 512, 512, out.data_ptr(), 512, M, 1, 2,
+                                         None, torch.cuda.current_stream().cuda_stream)
+    assert rc == _capi.SRBCRS_EINVAL and "flags" in _capi.lib().srbcrs_last_error().decode()
