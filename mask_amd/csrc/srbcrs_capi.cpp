@@ -1625,6 +1625,7 @@ int srbcrs_plan_tune_ex(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t 
                            std::array<int32_t, 3>{4, 16, 4}, std::array<int32_t, 3>{8, 32, 4}}) {
       srbcrs_run_opts o{};
       o.windows_per_wave = nz[0];
+      o.wg_cols = 64;
       o.tile_b = nz[1];
       o.depth = nz[2];
       o.grid_order = SRBCRS_GRID_NZSWEEP;
