@@ -145,6 +145,9 @@ EXPERIMENTS = {
     "lds_pad_40k": "SRBCRS_EXPERIMENT_LDS_PAD=40960",    # 40 KB of unused LDS per workgroup: at most 4 per CU
     "merged_pin": "SRBCRS_MERGED_SCHED_PIN",            # merged grid: loads pinned in source order (sched_barrier)
     "merged_vec_idx": "SRBCRS_MERGED_VEC_IDX",          # merged grid: each lane loads its B-row index pair
+    "nz_no_lds": "SRBCRS_EXPERIMENT_NZ_NO_LDS",         # nonzero sweep: gathers, values summed in registers
+    "nz_no_b": "SRBCRS_EXPERIMENT_NZ_NO_B",             # nonzero sweep: LDS read-add-writes, no B gathers
+    "nz_no_pin": "SRBCRS_NZ_NO_PIN",                    # nonzero sweep: no sched_barrier between loads and adds
 }
 
 

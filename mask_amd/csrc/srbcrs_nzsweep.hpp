@@ -135,8 +135,12 @@ __global__ __launch_bounds__(64) void spmm_nzsweep(const int* __restrict__ eoff,
         const uint32_t w = row_bcast(m[ms].x, q);
         // byte 0 = 16 i, byte 1 = the entry's top byte (the tile row)
         la[bs][q] = __builtin_amdgcn_perm(w, boff, 0x0c0c0700u);
+#ifdef SRBCRS_EXPERIMENT_NZ_NO_B
+        b[bs][q] = f4{__builtin_bit_cast(float, w), 1.f, 2.f, 3.f};
+#else
         b[bs][q] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(
                                               rs, __umul24(w, ldb4) + boff, 0, 0));   // the low 24 bits: the B row
+#endif
       }
     };
     // tile rows of one sub-batch are distinct (the dummy row aside), so its
@@ -147,6 +151,14 @@ __global__ __launch_bounds__(64) void spmm_nzsweep(const int* __restrict__ eoff,
     // gathers.  (LDS float atomics, ds_add_f32, ran the same work about ten
     // times slower.)
     f4 o[Q];
+#ifdef SRBCRS_EXPERIMENT_NZ_NO_LDS
+    f4 racc = f4{0.f, 0.f, 0.f, 0.f};
+    auto read = [&](int) {};
+    auto add = [&](int bs, int ms) {
+#pragma unroll
+      for (int q = 0; q < Q; ++q) racc += __builtin_bit_cast(float, row_bcast(m[ms].y, q)) * b[bs][q];
+    };
+#else
     auto read = [&](int bs) {
 #pragma unroll
       for (int q = 0; q < Q; ++q) o[q] = *reinterpret_cast<const f4*>(tileb + la[bs][q]);
@@ -159,6 +171,7 @@ __global__ __launch_bounds__(64) void spmm_nzsweep(const int* __restrict__ eoff,
         *reinterpret_cast<f4*>(tileb + la[bs][q]) = o[q] + p;
       }
     };
+#endif
     // the prologue in steady-state order (pairs, then gathers), pinned: the
     // loop's first wait then counts the same loads on both incoming paths
 #pragma unroll
@@ -179,6 +192,9 @@ __global__ __launch_bounds__(64) void spmm_nzsweep(const int* __restrict__ eoff,
         SRBCRS_NZ_PIN;
       }
     }
+#ifdef SRBCRS_EXPERIMENT_NZ_NO_LDS
+    tile4[lane] = racc;
+#endif
   }
   // the wave's own LDS writes are complete before its reads (LDS operations
   // of one wave execute in order)
