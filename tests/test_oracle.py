@@ -216,6 +216,31 @@ def test_csr_spmm_f32_within_bound():
     assert oracle.error_metrics(C_bad, C64, absAB)["max_ratio"] > 1e-4
 
 
+def test_csr_spmm_f32_is_the_unfused_sequential_sum():
+    """The fp32 oracle's exact arithmetic, which the nonzero sweep must match
+    bit for bit: per row, acc = fl(acc + fl(v * B[c])) in stored order from
+    +0, no fused multiply-add.  Restated with numpy float32 elementwise
+    operations (each rounded on its own); a fused multiply-add, a different
+    order or a pairwise sum would differ in some of these 64 x 48 outputs
+    (checked here for the fused form)."""
+    M, K, N = 64, 90, 48
+    rowptr, colind, values = random_csr(M, K, 0.3, 8)
+    B = np.random.default_rng(8).uniform(-1, 1, (K, N)).astype(np.float32)
+    want = np.zeros((M, N), np.float32)
+    fused = np.zeros((M, N), np.float32)
+    for r in range(M):
+        acc = np.zeros(N, np.float32)
+        accf = np.zeros(N, np.float32)
+        for e in range(rowptr[r], rowptr[r + 1]):
+            acc = acc + values[e] * B[colind[e]]
+            # v * b + acc with the product unrounded (the fused form, up to a float64 rounding)
+            accf = (np.float64(values[e]) * B[colind[e]].astype(np.float64) + accf).astype(np.float32)
+        want[r], fused[r] = acc, accf
+    got = oracle.csr_spmm_f32(rowptr, colind, values, B, M, nthreads=3)
+    assert np.array_equal(got, want)
+    assert not np.array_equal(got, fused)
+
+
 # ---- partitions (hand-worked) -------------------------------------------------
 
 def test_strict_lb_hand_case():
