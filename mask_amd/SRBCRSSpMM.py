@@ -111,6 +111,7 @@ class Plan:
         self.max_col = int(d.max_col)
         self.policy = ("row", 0)
         self.tuned_widths = set()   # widths srbcrs_plan_tune chose settings for (current schedule)
+        self._sweep_refused = set()   # operand layouts the nonzero sweep refused (run_sweep_if_sparse)
 
     @property
     def handle(self):
@@ -127,6 +128,33 @@ class Plan:
     def block_fill(self) -> float:
         """nnz / (blocks * blk_h * blk_w): the stored-value density."""
         return self.nnz / max(1, self.total_blocks * self.blk_h * self.blk_w)
+
+    def run_sweep_if_sparse(self, dense: Tensor, out: Tensor) -> bool:
+        """The low-block-density dispatch of the CSR fallback (SURVEY's "CSR
+        scalar/vector fallback for low block density", measured on an
+        MI355X): on a 16x8 plan with the compact copy whose block fill is
+        below SWEEP_FILL, run the nonzero sweep (grid order 5, default
+        knobs) into out and return True.  The library refuses, before any
+        launch, what the sweep cannot run (a split schedule, N, leading
+        dimensions, alignment, B's extent); then, and on denser plans,
+        return False and launch nothing.  Refusals are remembered per width
+        and operand layout."""
+        if self.blk_h != 16 or self.desc.stored_values < 0 or self.total_blocks == 0:
+            return False
+        if self.desc.stored_values >= SWEEP_FILL * self.total_blocks * self.blk_h * self.blk_w:
+            return False
+        key = (int(dense.shape[1]), int(dense.stride(0)), int(out.stride(0)), dense.data_ptr() % 16,
+               out.data_ptr() % 16, self.policy)
+        if key in self._sweep_refused:
+            return False
+        try:
+            self.run(dense, out, grid_order=5)
+        except _capi.SrbcrsError as e:
+            if e.code != _capi.SRBCRS_EINVAL:
+                raise
+            self._sweep_refused.add(key)
+            return False
+        return True
 
     def _operands(self, dense: Tensor, out: Optional[Tensor]) -> Tensor:
         """Validate dense (and out, allocated when None) before any launch:
@@ -302,6 +330,13 @@ def _preprocess(colind: Tensor, rowptr: Tensor, values: Tensor, num_nodes: int, 
     return row_window_offset, tcblock_rowid, tcblocktile_id, tcblock_offset, sparse_a_to_x_idx, total
 
 
+# Block fill (stored values / (blocks * 128)) below which the nonzero sweep
+# beats the tuned MFMA kernels at N = 512 on one MI355X: uniform-like rows
+# with window-clustered columns, sweep against tuned MFMA (ms): fill 0.062
+# 0.157 / 0.214, 0.095 0.154 / 0.156, 0.137 0.150 / 0.121, 0.250 0.147 / 0.082.
+SWEEP_FILL = 0.125
+
+
 def _tile_b_for(n: int) -> int:
     """SRBCRS_TILE_B handling (SRBCRSSpMM_kernel.cu:435-475): validates the
     forced tile, else picks 64/32/16 by divisibility; 0 = none fits."""
@@ -365,12 +400,12 @@ def _run(dense: Tensor, row_window_offset: Tensor, tcblocktile_id: Tensor, tcblo
     # no schedule requested: "auto" (split on heavy-tailed windows, else one task per window)
     plan.set_schedule(*(sched or ("auto", 0)))
     out = torch.empty((entry.num_nodes, n), dtype=torch.float32, device=dense.device)
+    # the reference's CSR-fallback opt-in also admits the CSR product's bits
+    # on the SR-BCRS path: the nonzero sweep, for low block density
+    csr_ok = os.environ.get("SPARSENE_ALLOW_CSR_FALLBACK", "0") == "1"
     if os.environ.get("SPARSENE_SRBCRS_AUTOTUNE", "0") == "1" and n not in plan.tuned_widths:
-        # once per (width, schedule); the product lands in out.  With the
-        # reference's CSR-fallback opt-in the nonzero sweep (the CSR
-        # product's bits) competes too.
-        plan.tune(dense, out, nonzero_sweep=os.environ.get("SPARSENE_ALLOW_CSR_FALLBACK", "0") == "1")
-    else:
+        plan.tune(dense, out, nonzero_sweep=csr_ok)   # once per (width, schedule); the product lands in out
+    elif n in plan.tuned_widths or not (csr_ok and plan.run_sweep_if_sparse(dense, out)):
         plan.run(dense, out)
     return [out]
 

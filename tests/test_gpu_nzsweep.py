@@ -250,3 +250,42 @@ def test_tune_ex_admits_the_sweep(gpu):
     rc = _capi.lib().srbcrs_plan_tune_ex(plan.handle, dB.data_ptr(), K, 512, 512, out.data_ptr(), 512, M, 1, 2,
                                          None, torch.cuda.current_stream().cuda_stream)
     assert rc == _capi.SRBCRS_EINVAL and "flags" in _capi.lib().srbcrs_last_error().decode()
+
+
+def test_dropin_dispatch_under_csr_fallback(gpu, monkeypatch):
+    """run_SRBCRS_16x8 with SPARSENE_ALLOW_CSR_FALLBACK=1 runs the nonzero
+    sweep on low-block-fill plans (bits = the fp32 CSR oracle's) and the MFMA
+    kernels on dense-block plans, on widths the sweep refuses and without the
+    opt-in (bits = the default run's)."""
+    import torch
+    from mask_amd import SRBCRSSpMM as S
+
+    def run(rowptr, colind, values, M, K, N, seed):
+        B = np.random.default_rng(seed).uniform(-1, 1, (K, N)).astype(np.float32)
+        ci, rp, vv = (torch.from_numpy(a).cuda() for a in (colind, rowptr, values))
+        z = torch.zeros(1, dtype=torch.int32, device="cuda")
+        rwo, _, tid, toff, a2x, _ = S.preprocess_gpu_16x8(ci, rp, vv, M, 16, 8, z, z, z)
+        dB = torch.from_numpy(B).cuda()
+        (out,) = S.run_SRBCRS_16x8(dB, rwo, tid, toff, a2x, M, int(colind.size), "")
+        plan = S.plan_for(rwo)
+        return out.cpu().numpy(), plan.run(dB).cpu().numpy(), oracle.csr_spmm_f32(rowptr, colind, values, B, M)
+
+    M = K = 2048
+    sparse = random_csr(M, K, 0.004, seed=51)             # ~1 value per block column: fill ~0.06
+    rng = np.random.default_rng(52)                       # dense 16x8 blocks on the diagonal: fill 1
+    rows = np.repeat(np.arange(M), 8)
+    cols = (rows // 8) * 8 + np.tile(np.arange(8), M)
+    rp = np.zeros(M + 1, np.int32)
+    rp[1:] = np.cumsum(np.bincount(rows, minlength=M))
+    dense_blocks = (rp, cols.astype(np.int32), rng.uniform(-1, 1, cols.size).astype(np.float32))
+    _say("dispatch")
+    monkeypatch.setenv("SPARSENE_ALLOW_CSR_FALLBACK", "1")
+    got, mfma, csr = run(*sparse, M, K, 128, 1)
+    assert np.array_equal(got, csr) and not np.array_equal(got, mfma)
+    got, mfma, csr = run(*sparse, M, K, 96, 2)            # N % 64 != 0: refused, MFMA default
+    assert np.array_equal(got, mfma)
+    got, mfma, csr = run(*dense_blocks, M, K, 128, 3)
+    assert np.array_equal(got, mfma)
+    monkeypatch.delenv("SPARSENE_ALLOW_CSR_FALLBACK")
+    got, mfma, csr = run(*sparse, M, K, 128, 4)
+    assert np.array_equal(got, mfma)
