@@ -83,6 +83,10 @@ def parse():
     ap.add_argument("--gather-study", action="store_true",
                     help="only time the gather probe on the workload's own B-row index stream: unit order vs "
                          "units of W windows merged by column, over grids and column-chunk widths")
+    ap.add_argument("--sweep-crossover", action="store_true",
+                    help="only time the nonzero sweep against the tuned MFMA kernels on 65536-row matrices of "
+                         "16 values per row whose window columns are clustered to set the block fill (the "
+                         "low-density dispatch threshold, SRBCRSSpMM.SWEEP_FILL)")
     ap.add_argument("--copy-calibration-mb", type=int, default=0,
                     help="only run an elementwise copy of this many MiB (5 launches) to calibrate "
                          "rocprofv3 FETCH_SIZE / WRITE_SIZE against a known byte count")
@@ -363,6 +367,70 @@ def _pct(v):
         return float(v)
     except (TypeError, ValueError):
         return None
+
+
+def _clustered_rows(M, K, per_row, pool, seed):
+    """M rows of per_row distinct sorted columns; the rows of each 16-row
+    window draw them from one set of `pool` window columns (pool None: from
+    all K), so the SR-BCRS 16x8 block fill is about per_row / pool."""
+    rng = np.random.default_rng(seed)
+    cols = np.empty((M, per_row), np.int64)
+    for w in range(M // 16):
+        src = rng.choice(K, pool, replace=False) if pool else None
+        for r in range(16):
+            cols[16 * w + r] = np.sort(rng.choice(src, per_row, replace=False) if pool
+                                       else rng.choice(K, per_row, replace=False))
+    rowptr = (np.arange(M + 1) * per_row).astype(np.int32)
+    return rowptr, cols.reshape(-1).astype(np.int32), rng.uniform(-1, 1, M * per_row).astype(np.float32)
+
+
+def sweep_crossover(args):
+    """The nonzero sweep (grid order 5, default knobs) against the MFMA
+    kernels at the setting srbcrs_plan_tune picks, on 65536 x 65536 matrices
+    of 16 values per row at block fills from 0.06 to 0.5, N = 512: sustained
+    ms per launch (--sustained-s of back-to-back launches each, after the
+    tuning and 20 warm-up launches).  One JSON line."""
+    import torch
+    from mask_amd.SRBCRSSpMM import Plan
+    M = K = 65536
+    N = args.N or 512
+    dev = torch.device("cuda", 0)
+    B = torch.rand((K, N), device=dev) * 2 - 1
+    C = torch.empty((M, N), device=dev)
+    secs = args.sustained_s if args.sustained_s > 0 else 1.0
+
+    def sustained(fn):
+        for _ in range(20):
+            fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        n = 0
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        while time.perf_counter() - t0 < secs:
+            for _ in range(50):
+                fn()
+            n += 50
+            torch.cuda.synchronize()
+        e1.record()
+        torch.cuda.synchronize()
+        return round(e0.elapsed_time(e1) / n, 5)
+
+    rows = []
+    for pool in (None, 256, 128, 64, 32):
+        rp, ci, vv = _clustered_rows(M, K, 16, pool, seed=5)
+        plan = Plan(torch.from_numpy(rp).to(dev), torch.from_numpy(ci).to(dev), torch.from_numpy(vv).to(dev), M)
+        fill = int(rp[-1]) / (plan.total_blocks * 128)
+        tk = plan.tune(B, C, reps=3)
+        ms_mfma = sustained(lambda: plan.run(B, C))
+        ms_sweep = sustained(lambda: plan.run(B, C, grid_order=NZSWEEP))
+        rows.append({"window_pool": pool, "block_fill": round(fill, 4), "mfma_tuned": tk, "mfma_ms": ms_mfma,
+                     "sweep_ms": ms_sweep, "sweep_faster": ms_sweep < ms_mfma})
+        print(f"[crossover] pool={pool} fill={fill:.3f} mfma={ms_mfma} sweep={ms_sweep}", file=sys.stderr,
+              flush=True)
+        del plan
+        torch.cuda.empty_cache()
+    print(json.dumps({"sweep_crossover": rows, "N": N, "rows_per_matrix": M, "values_per_row": 16}), flush=True)
 
 
 def umc_measure(args):
@@ -777,6 +845,9 @@ def main():
         return
     if args.gather_study:
         gather_study(args)
+        return
+    if args.sweep_crossover:
+        sweep_crossover(args)
         return
 
     if args.umc_seconds > 0:

@@ -331,9 +331,10 @@ def _preprocess(colind: Tensor, rowptr: Tensor, values: Tensor, num_nodes: int, 
 
 
 # Block fill (stored values / (blocks * 128)) below which the nonzero sweep
-# beats the tuned MFMA kernels at N = 512 on one MI355X: uniform-like rows
-# with window-clustered columns, sweep against tuned MFMA (ms): fill 0.062
-# 0.157 / 0.214, 0.095 0.154 / 0.156, 0.137 0.150 / 0.121, 0.250 0.147 / 0.082.
+# beats the tuned MFMA kernels at N = 512 on one MI355X (bench.py
+# --sweep-crossover, 16 values per row, window-clustered columns; sustained ms,
+# sweep / tuned MFMA): fill 0.062 0.138 / 0.213, 0.095 0.138 / 0.157, 0.137
+# 0.137 / 0.121, 0.250 0.138 / 0.082.
 SWEEP_FILL = 0.125
 
 
