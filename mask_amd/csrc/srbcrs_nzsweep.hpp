@@ -119,7 +119,7 @@ __global__ __launch_bounds__(64) void spmm_nzsweep(const int* __restrict__ eoff,
   const int64_t e0 = uniform_load(eoff, g), e1 = uniform_load(eoff, g + 1);
   if (e0 < e1) {
     const __amdgpu_buffer_rsrc_t rs =
-        __builtin_amdgcn_make_buffer_rsrc((void*)(B + col0), 0, 0x7fffffff, 0x00020000);
+        __builtin_amdgcn_make_buffer_rsrc((void*)(B + col0), 0, (int)0xffffffffu, 0x00020000);   // 4 GiB
     const uint32_t ldb4 = (uint32_t)(ldb * 4);
     const uint32_t boff = (uint32_t)sub * 16u;
     const int64_t n_sb = (e1 - e0) / U;

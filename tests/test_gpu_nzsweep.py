@@ -289,3 +289,36 @@ def test_dropin_dispatch_under_csr_fallback(gpu, monkeypatch):
     monkeypatch.delenv("SPARSENE_ALLOW_CSR_FALLBACK")
     got, mfma, csr = run(*sparse, M, K, 128, 4)
     assert np.array_equal(got, mfma)
+
+
+def test_nzsweep_b_beyond_2gib(gpu):
+    """B rows whose byte offsets pass 2^31 (K * ldb * 4 between 2 and 4 GiB,
+    which the 32-bit buffer offsets allow): B is a 64-column view of a
+    600000 x 1024 buffer (2.46 GB), and rows reference columns above 524288
+    (offsets above 2^31).  Equal to the oracle's fp32 product bit for bit."""
+    import torch
+    rng = np.random.default_rng(61)
+    M, K, N, LD = 4096, 600000, 64, 1024
+    rows = []
+    for c in rng.integers(0, 12, size=M):
+        # about half of each row's columns in the top eighth of B
+        cand = np.concatenate([rng.choice(K, c // 2 + 1, replace=False), rng.integers(K - K // 8, K, c // 2 + 1)])
+        rows.append(np.sort(np.unique(cand))[:c])
+    rowptr = np.zeros(M + 1, np.int64)
+    rowptr[1:] = np.cumsum([r.size for r in rows])
+    rowptr = rowptr.astype(np.int32)
+    colind = np.concatenate(rows).astype(np.int32)
+    values = rng.uniform(-1, 1, colind.size).astype(np.float32)
+    assert int(colind.max()) * LD * 4 >= 2 ** 31
+    B = rng.uniform(-1, 1, (K, N)).astype(np.float32)
+    big = torch.zeros((K, LD), device="cuda")
+    big[:, :N] = torch.from_numpy(B).cuda()
+    dB = big[:, :N]
+    plan = _plan(rowptr, colind, values, M)
+    _say("nzsweep beyond 2 GiB", K, LD)
+    out = torch.full((M, N), float("nan"), device="cuda")
+    plan.run(dB, out, grid_order=NZ)
+    want = oracle.csr_spmm_f32(rowptr, colind, values, B, M)
+    assert np.array_equal(out.cpu().numpy(), want)
+    del big, dB
+    torch.cuda.empty_cache()
