@@ -333,8 +333,8 @@ def _preprocess(colind: Tensor, rowptr: Tensor, values: Tensor, num_nodes: int, 
 # Block fill (stored values / (blocks * 128)) below which the nonzero sweep
 # beats the tuned MFMA kernels at N = 512 on one MI355X (bench.py
 # --sweep-crossover, 16 values per row, window-clustered columns; sustained ms,
-# sweep / tuned MFMA): fill 0.062 0.138 / 0.213, 0.095 0.138 / 0.157, 0.137
-# 0.137 / 0.121, 0.250 0.138 / 0.082.
+# sweep / tuned MFMA): fill 0.062 0.136 / 0.213, 0.095 0.136 / 0.158, 0.137
+# 0.135 / 0.121, 0.250 0.136 / 0.082.
 SWEEP_FILL = 0.125
 
 

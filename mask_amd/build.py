@@ -148,6 +148,7 @@ EXPERIMENTS = {
     "nz_no_lds": "SRBCRS_EXPERIMENT_NZ_NO_LDS",         # nonzero sweep: gathers, values summed in registers
     "nz_no_b": "SRBCRS_EXPERIMENT_NZ_NO_B",             # nonzero sweep: LDS read-add-writes, no B gathers
     "nz_no_pin": "SRBCRS_NZ_NO_PIN",                    # nonzero sweep: no sched_barrier between loads and adds
+    "nz_plain_c_store": "SRBCRS_NZ_PLAIN_C_STORE",      # nonzero sweep: C written with plain stores
 }
 
 

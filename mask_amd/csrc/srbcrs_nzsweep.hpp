@@ -128,6 +128,7 @@ __global__ __launch_bounds__(64) void spmm_nzsweep(const int* __restrict__ eoff,
     uint2 m[P];
     f4 b[D][Q];
     uint32_t la[D][Q];   // LDS byte offsets of the gathered rows' tile rows
+    // (nontemporal pair loads ran 35 % slower: 0.181 against 0.134 ms)
     auto fetch = [&](int ms, int64_t j) { m[ms] = gp[(j < n_sb ? j : n_sb - 1) * U]; };
     auto issue = [&](int bs, int ms) {
 #pragma unroll
@@ -204,7 +205,12 @@ __global__ __launch_bounds__(64) void spmm_nzsweep(const int* __restrict__ eoff,
     const int64_t row = row0 + r;
     if (row < M) {
       const int64_t orow = rowmap ? rowmap[row] : row;
+#ifdef SRBCRS_NZ_PLAIN_C_STORE
       *reinterpret_cast<f4*>(C + orow * ldc + col0 + 4 * sub) = tile4[r * 16 + sub];
+#else
+      // C is written once: nontemporal, so that it does not push B's rows out of the L2
+      __builtin_nontemporal_store(tile4[r * 16 + sub], reinterpret_cast<f4*>(C + orow * ldc + col0 + 4 * sub));
+#endif
     }
   }
 }
