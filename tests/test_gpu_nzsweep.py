@@ -270,6 +270,8 @@ def test_dropin_dispatch_under_csr_fallback(gpu, monkeypatch):
         plan = S.plan_for(rwo)
         return out.cpu().numpy(), plan.run(dB).cpu().numpy(), oracle.csr_spmm_f32(rowptr, colind, values, B, M)
 
+    # the GCN bridge leaves SRBCRS_TILE_B set for the module, as the reference's does
+    monkeypatch.delenv("SRBCRS_TILE_B", raising=False)
     M = K = 2048
     sparse = random_csr(M, K, 0.004, seed=51)             # ~1 value per block column: fill ~0.06
     rng = np.random.default_rng(52)                       # dense 16x8 blocks on the diagonal: fill 1
