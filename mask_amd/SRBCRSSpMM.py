@@ -130,9 +130,9 @@ class Plan:
         return self.nnz / max(1, self.total_blocks * self.blk_h * self.blk_w)
 
     def run_sweep_if_sparse(self, dense: Tensor, out: Tensor) -> bool:
-        """The low-block-density dispatch of the CSR fallback (SURVEY's "CSR
-        scalar/vector fallback for low block density", measured on an
-        MI355X): on a 16x8 plan with the compact copy whose block fill is
+        """The low-block-density dispatch of the CSR fallback (the vector
+        kernel for low block density, threshold measured on an MI355X): on
+        a 16x8 plan with the compact copy whose block fill is
         below SWEEP_FILL, run the nonzero sweep (grid order 5, default
         knobs) into out and return True.  The library refuses, before any
         launch, what the sweep cannot run (a split schedule, N, leading
