@@ -324,3 +324,26 @@ def test_nzsweep_b_beyond_2gib(gpu):
     assert np.array_equal(out.cpu().numpy(), want)
     del big, dB
     torch.cuda.empty_cache()
+
+
+def test_nzsweep_empty_matrix_and_wide_c(gpu):
+    """A matrix without stored values writes zeros to every row; C with a
+    leading dimension above N (a view of a wider buffer) keeps the columns
+    outside the view untouched."""
+    import torch
+    M, K, N = 300, 400, 128
+    rowptr = np.zeros(M + 1, np.int32)
+    plan = _plan(rowptr, np.zeros(0, np.int32), np.zeros(0, np.float32), M)
+    dB = torch.ones((K, N), device="cuda")
+    out = torch.full((M, N), 7.0, device="cuda")
+    _say("nzsweep empty")
+    plan.run(dB, out, grid_order=NZ)
+    assert bool((out == 0).all())
+    rowptr, colind, values = random_csr(M, K, 0.03, seed=71)
+    B = np.random.default_rng(71).uniform(-1, 1, (K, N)).astype(np.float32)
+    plan = _plan(rowptr, colind, values, M)
+    wide = torch.full((M, 3 * N), 7.0, device="cuda")
+    plan.run(torch.from_numpy(B).cuda(), wide[:, N:2 * N], grid_order=NZ)
+    got = wide.cpu().numpy()
+    assert np.array_equal(got[:, N:2 * N], oracle.csr_spmm_f32(rowptr, colind, values, B, M))
+    assert (got[:, :N] == 7.0).all() and (got[:, 2 * N:] == 7.0).all()
