@@ -1,9 +1,9 @@
 /* A plain C99 client of the C ABI (include/srbcrs.h), test infrastructure:
  * builds a seeded random CSR on the host, converts it (host CSR, then the
  * device converter from HBM), runs the SpMM with default and tuned launch
- * settings, and checks C against a double-precision loop on the host with
- * the fp32 gate |C - C64| <= 1e-4 * (|A||B|).  Prints "C-ABI OK" and
- * returns 0 on success. */
+ * settings and the nonzero sweep, and checks C against a double-precision
+ * loop on the host with the fp32 gate |C - C64| <= 1e-4 * (|A||B|).
+ * Prints "C-ABI OK" and returns 0 on success. */
 #include <hip/hip_runtime_api.h>
 #include <math.h>
 #include <stdint.h>
@@ -107,6 +107,19 @@ int main(void) {
     CHECK(srbcrs_plan_tune(plan, dB, K, N, N, dC, N, M, 2, &best, NULL));
     HIPCHECK(hipMemset(dC, 0, sizeof(float) * M * N));
     CHECK(srbcrs_run(plan, dB, K, N, N, dC, N, M, NULL));   /* uses the tuned setting */
+    HIPCHECK(hipMemcpy(C, dC, sizeof(float) * M * N, hipMemcpyDeviceToHost));
+    if (check(C, rp, ci, v, B, M, N)) return 1;
+    /* the nonzero sweep (grid order 5, row schedule), then the tuner with it admitted */
+    CHECK(srbcrs_plan_set_schedule(plan, "row", 0));
+    srbcrs_run_opts sweep = {0};
+    sweep.grid_order = SRBCRS_GRID_NZSWEEP;
+    HIPCHECK(hipMemset(dC, 0, sizeof(float) * M * N));
+    CHECK(srbcrs_run_ex(plan, dB, K, N, N, dC, N, M, &sweep, NULL));
+    HIPCHECK(hipMemcpy(C, dC, sizeof(float) * M * N, hipMemcpyDeviceToHost));
+    if (check(C, rp, ci, v, B, M, N)) return 1;
+    CHECK(srbcrs_plan_tune_ex(plan, dB, K, N, N, dC, N, M, 2, SRBCRS_TUNE_NONZERO_SWEEP, &best, NULL));
+    HIPCHECK(hipMemset(dC, 0, sizeof(float) * M * N));
+    CHECK(srbcrs_run(plan, dB, K, N, N, dC, N, M, NULL));
     HIPCHECK(hipMemcpy(C, dC, sizeof(float) * M * N, hipMemcpyDeviceToHost));
     if (check(C, rp, ci, v, B, M, N)) return 1;
     /* an error path: N not a multiple of 16 */
