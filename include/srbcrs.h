@@ -267,7 +267,10 @@ int srbcrs_plan_trim(srbcrs_plan *plan, void *stream);
  *                multiple of 64 with N / 64 dividing 8 or a multiple of 8,
  *                ldb and ldc multiples of 4, 16-byte aligned B and C,
  *                K * ldb * 4 < 2^32, ldb * 4 < 2^24 and column indices
- *                below 2^24.  C[r, :] is the sum of fl(v * B[c, :]) over
+ *                below 2^24; a matrix whose stream would be mostly
+ *                padding (a row with far more values than its group's
+ *                others: over 8 entries per value and 2^22 entries) is
+ *                refused.  C[r, :] is the sum of fl(v * B[c, :]) over
  *                the row's stored values in ascending column order, each
  *                product rounded before it is added (the fp32 CSR product,
  *                not the MFMA kernels' bits).  The first run per setting

@@ -855,6 +855,14 @@ const srbcrs_plan::Nz& nz_stream(srbcrs_plan& plan, int W, int U, int D, hipStre
     if (entries > INT32_MAX) fail(SRBCRS_EINVAL, "the nonzero-sweep stream exceeds 2^31 entries");
     eoff[(size_t)g + 1] = (int32_t)entries;
   }
+  // a row with many more values than its group's other rows puts one value
+  // per sub-batch and fills the rest with padding (up to U entries per
+  // value): refuse a stream that would be mostly padding and large (the
+  // MFMA grids serve such matrices)
+  if (entries > std::max<int64_t>(8 * plan.n_apacked, (int64_t)1 << 22) + (int64_t)2 * D * U * n_groups)
+    fail(SRBCRS_EINVAL, "the nonzero sweep would pad this matrix to %lld entries for %lld values (rows much "
+                        "longer than their group's others): use another grid order", (long long)entries,
+         (long long)plan.n_apacked);
   std::vector<uint2> pairs((size_t)entries);
   parallel_for(n_groups, [&](int64_t lo, int64_t hi) {
     for (int64_t g = lo; g < hi; ++g)

@@ -347,3 +347,30 @@ def test_nzsweep_empty_matrix_and_wide_c(gpu):
     got = wide.cpu().numpy()
     assert np.array_equal(got[:, N:2 * N], oracle.csr_spmm_f32(rowptr, colind, values, B, M))
     assert (got[:, :N] == 7.0).all() and (got[:, 2 * N:] == 7.0).all()
+
+
+def test_nzsweep_refuses_a_stream_of_padding(gpu):
+    """One row far longer than its group's others would put one of its values
+    per sub-batch and pad the rest (200000 values, 6.4 M entries): the sweep
+    refuses before any launch (C untouched), and the drop-in's dispatch falls
+    back to the MFMA kernels."""
+    import torch
+    from mask_amd._capi import SrbcrsError
+    rng = np.random.default_rng(81)
+    M, K, N = 64, 300000, 64
+    rows = [np.sort(rng.choice(K, 200000, replace=False))] + [np.sort(rng.choice(K, 2, replace=False))
+                                                              for _ in range(M - 1)]
+    rowptr = np.zeros(M + 1, np.int32)
+    rowptr[1:] = np.cumsum([r.size for r in rows])
+    colind = np.concatenate(rows).astype(np.int32)
+    values = rng.uniform(-1, 1, colind.size).astype(np.float32)
+    plan = _plan(rowptr, colind, values, M)
+    dB = torch.ones((K, N), device="cuda")
+    out = torch.full((M, N), 7.0, device="cuda")
+    _say("nzsweep padding refusal")
+    with pytest.raises(SrbcrsError, match="pad"):
+        plan.run(dB, out, grid_order=NZ)
+    torch.cuda.synchronize()
+    assert bool((out == 7.0).all())
+    assert not plan.run_sweep_if_sparse(dB, out)
+    assert bool((out == 7.0).all())
