@@ -274,7 +274,8 @@ int srbcrs_plan_trim(srbcrs_plan *plan, void *stream);
  *                the row's stored values in ascending column order, each
  *                product rounded before it is added (the fp32 CSR product,
  *                not the MFMA kernels' bits).  The first run per setting
- *                builds its value stream on the host (it allocates);
+ *                builds its value stream on the host (it allocates; kept
+ *                until the plan is destroyed);
  *   windows_per_wave  "row" schedule: consecutive row windows one wave
  *                streams through its register ring (0 = 1), in [0, 4096];
  *   a_operand    see SRBCRS_A_* below;
