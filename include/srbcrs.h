@@ -264,9 +264,10 @@ int srbcrs_plan_trim(srbcrs_plan *plan, void *stream);
  *                tile_b = values per sub-batch (16, 32 or 64; 0 = 32),
  *                depth = sub-batches of gathers in flight (2 or 4; 0 = 2;
  *                4 only with tile_b 16 or 32); wg_cols 0 or 64.  Needs N a
- *                multiple of 64 with N / 64 dividing 8 or a multiple of 8,
- *                ldb and ldc multiples of 4, 16-byte aligned B and C,
- *                K * ldb * 4 < 2^32, ldb * 4 < 2^24 and column indices
+ *                multiple of 64 (each 64-column chunk pinned to one XCD
+ *                when N / 64 divides 8 or is a multiple of 8, unpinned
+ *                otherwise), ldb and ldc multiples of 4, 16-byte aligned
+ *                B and C, K * ldb * 4 < 2^32, ldb * 4 < 2^24 and column indices
  *                below 2^24; a matrix whose stream would be mostly
  *                padding (a row with far more values than its group's
  *                others: over 8 entries per value and 2^22 entries) is

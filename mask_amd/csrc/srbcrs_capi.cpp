@@ -1384,9 +1384,7 @@ static void run_impl(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
       if (!srbcrs::nz_setting_ok(W, U, D))
         fail(SRBCRS_EINVAL, "the nonzero sweep takes windows_per_wave 4 or 8 and (tile_b, depth) (16, 2), (16, 4), "
                             "(32, 2), (32, 4) or (64, 2) (got %d, %d, %d)", W, U, D);
-      if (N % 64 || !srbcrs::merged_chunks_ok((int)(N / 64)))
-        fail(SRBCRS_EINVAL, "the nonzero sweep needs N a multiple of 64 with N / 64 column chunks dividing 8 or a "
-                            "multiple of 8");
+      if (N % 64) fail(SRBCRS_EINVAL, "the nonzero sweep needs N a multiple of 64 (got %lld)", (long long)N);
       if (N % 4 || ldb % 4 || ldc % 4 || (reinterpret_cast<uintptr_t>(d_B) | reinterpret_cast<uintptr_t>(d_C)) % 16)
         fail(SRBCRS_EINVAL, "the nonzero sweep needs ldb, ldc multiples of 4 and 16-byte aligned B and C");
       if ((uint64_t)K * (uint64_t)ldb * 4u >= (1ull << 32) || (uint64_t)ldb * 4u >= (1ull << 24))

@@ -102,11 +102,12 @@ hipError_t launch_tasks_compact(const StreamArgs& a, const TaskTable& t, int vec
 hipError_t launch_merged(const MergedArgs& m, const StreamArgs& a, int cols, int depth, hipStream_t st);
 bool merged_setting_ok(int cols, int W, int depth);
 bool merged_chunks_ok(int n_chunks);
-// grid of the merged-window kernels: rounds of 8 workgroups, one per XCD
+// grid of the merged-window kernels: rounds of 8 workgroups, one per XCD,
+// for chunk counts merged_chunks_ok accepts; one workgroup per (group, chunk)
+// otherwise
 int64_t merged_grid(int64_t n_groups, int n_chunks);
-// spmm_nzsweep: W 4, 8 or 16, (U, D) = (tile_b, depth) one of
-// nz_setting_ok's, a.N / 64 column chunks, which merged_chunks_ok must
-// accept.
+// spmm_nzsweep: W 4 or 8, (U, D) = (tile_b, depth) one of nz_setting_ok's,
+// a.N / 64 column chunks (XCD-pinned when merged_chunks_ok accepts the count).
 hipError_t launch_nzsweep(const NzArgs& z, const StreamArgs& a, int U, int D, hipStream_t st);
 bool nz_setting_ok(int W, int U, int D);
 hipError_t launch_reduce(const ReduceArgs& a, int vec, hipStream_t st);

@@ -7,8 +7,10 @@
 
 namespace srbcrs {
 
-// Grid of spmm_merged: rounds of 8 workgroups, one per XCD (see xcd_chunk).
+// Grid of spmm_merged: rounds of 8 workgroups, one per XCD (see xcd_chunk),
+// or one workgroup per (group, chunk) for chunk counts xcd_chunk does not pin.
 int64_t merged_grid(int64_t n_groups, int n_chunks) {
+  if (!merged_chunks_ok(n_chunks)) return n_groups * n_chunks;
   if (n_chunks <= kNumXcd) {
     const int per = kNumXcd / n_chunks;
     return (n_groups + per - 1) / per * kNumXcd;

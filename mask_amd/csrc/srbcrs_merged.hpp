@@ -70,12 +70,16 @@ struct MergedRows {
 // Workgroup id -> (window group g, column chunk c) with the chunk pinned to
 // the XCD the dispatcher deals the workgroup to (id % 8).  n_chunks divides
 // 8 (XCD x serves chunk x % n_chunks, 8 / n_chunks groups per round of 8
-// workgroups) or is a multiple of 8 (XCD x serves chunks x, x + 8, ...).
-// Returns false for the padding workgroups of the last round.
+// workgroups) or is a multiple of 8 (XCD x serves chunks x, x + 8, ...);
+// any other count runs unpinned, the chunks of a group on consecutive
+// workgroups.  Returns false for the padding workgroups of the last round.
 __device__ __forceinline__ bool xcd_chunk(int64_t bid, int n_chunks, int64_t n_groups, int64_t& g, int& c) {
   const int x = (int)(bid % kNumXcd);
   const int64_t t = bid / kNumXcd;
-  if (n_chunks <= kNumXcd) {
+  if (n_chunks <= kNumXcd ? kNumXcd % n_chunks != 0 : n_chunks % kNumXcd != 0) {
+    c = (int)(bid % n_chunks);
+    g = bid / n_chunks;
+  } else if (n_chunks <= kNumXcd) {
     const int per = kNumXcd / n_chunks;
     c = x % n_chunks;
     g = t * per + x / n_chunks;

@@ -42,6 +42,8 @@ def _run(plan, dB, M, N, W, U, D):
     (640, 700, 128, 0.03, 2),
     (257, 257, 1024, 0.02, 3),              # 16 chunks of 64 columns: two per XCD
     (900, 2500, 64, 0.01, 4),               # one chunk
+    (500, 900, 192, 0.02, 6),               # 3 chunks: not XCD-pinned
+    (333, 600, 640, 0.02, 7),               # 10 chunks: not XCD-pinned
 ])
 def test_nzsweep_equals_fp32_csr_oracle(gpu, M, K, N, density, seed):
     import torch
@@ -127,7 +129,6 @@ def test_nzsweep_refusals_leave_c_untouched(gpu):
     rowptr, colind, values = random_csr(M, K, 0.03, seed=5)
     plan = _plan(rowptr, colind, values, M)
     cases = [
-        (192, dict(), "divid"),                                  # 3 chunks of 64
         (96, dict(), "multiple of 64"),
         (128, dict(windows_per_wave=2), "windows_per_wave"),
         (128, dict(windows_per_wave=16), "windows_per_wave"),
