@@ -784,12 +784,22 @@ const srbcrs_plan::Nz& nz_stream(srbcrs_plan& plan, int W, int U, int D, hipStre
   }
   const uint32_t dummy = (uint32_t)(16 * W);
   const int64_t n_groups = (Mo + W - 1) / W;
+  // a row with many more values than its group's other rows puts one value
+  // per sub-batch and fills the rest with padding (up to U entries per
+  // value): a stream that would be mostly padding and large is refused (the
+  // MFMA grids serve such matrices), before it is built when the groups'
+  // lower bounds (U entries per sub-batch, at least as many sub-batches as
+  // the longest row has values) already exceed the limit
+  const int64_t limit = std::max<int64_t>(8 * plan.n_apacked, (int64_t)1 << 22) + (int64_t)kChunk * n_groups;
+  std::atomic<int64_t> bound{0};
+  std::atomic<bool> over{false};
   std::vector<std::vector<uint2>> g_pairs((size_t)n_groups);
   parallel_for(n_groups, [&](int64_t lo, int64_t hi) {
     std::vector<uint32_t> le;
     std::vector<float> lv;
     std::vector<char> taken;
     for (int64_t g = lo; g < hi; ++g) {
+      if (over.load(std::memory_order_relaxed)) return;
       // the group's values in list order
       le.clear();
       lv.clear();
@@ -812,6 +822,15 @@ const srbcrs_plan::Nz& nz_stream(srbcrs_plan& plan, int W, int U, int D, hipStre
               lv.push_back(packed[(size_t)wd.y + __builtin_popcount(wd.x & ((1u << bit) - 1u))]);
             }
         }
+      {
+        int count[256] = {0}, longest = 0;
+        for (const uint32_t e : le) longest = std::max(longest, ++count[e >> kRowShift]);
+        const int64_t batches = std::max<int64_t>(((int64_t)le.size() + U - 1) / U, longest);
+        if (bound.fetch_add(batches * U, std::memory_order_relaxed) + batches * U > limit) {
+          over.store(true, std::memory_order_relaxed);
+          return;
+        }
+      }
       // sub-batches of U distinct tile rows, each stored transposed: pair
       // gg * Q + q = entry E * q + gg
       std::vector<uint2>& op = g_pairs[(size_t)g];
@@ -848,6 +867,11 @@ const srbcrs_plan::Nz& nz_stream(srbcrs_plan& plan, int W, int U, int D, hipStre
       while (op.size() % kChunk) op.push_back(uint2{(dummy << kRowShift) | prev, 0u});
     }
   });
+#define SRBCRS_NZ_PADDED(what)                                                                              \
+  "the nonzero sweep would pad this matrix to " what " entries for %lld values (rows much longer than their " \
+  "group's others): use another grid order"
+  if (over.load())
+    fail(SRBCRS_EINVAL, SRBCRS_NZ_PADDED("over %lld"), (long long)limit, (long long)plan.n_apacked);
   std::vector<int32_t> eoff((size_t)n_groups + 1, 0);
   int64_t entries = 0;
   for (int64_t g = 0; g < n_groups; ++g) {
@@ -855,14 +879,8 @@ const srbcrs_plan::Nz& nz_stream(srbcrs_plan& plan, int W, int U, int D, hipStre
     if (entries > INT32_MAX) fail(SRBCRS_EINVAL, "the nonzero-sweep stream exceeds 2^31 entries");
     eoff[(size_t)g + 1] = (int32_t)entries;
   }
-  // a row with many more values than its group's other rows puts one value
-  // per sub-batch and fills the rest with padding (up to U entries per
-  // value): refuse a stream that would be mostly padding and large (the
-  // MFMA grids serve such matrices)
-  if (entries > std::max<int64_t>(8 * plan.n_apacked, (int64_t)1 << 22) + (int64_t)2 * D * U * n_groups)
-    fail(SRBCRS_EINVAL, "the nonzero sweep would pad this matrix to %lld entries for %lld values (rows much "
-                        "longer than their group's others): use another grid order", (long long)entries,
-         (long long)plan.n_apacked);
+  if (entries > limit) fail(SRBCRS_EINVAL, SRBCRS_NZ_PADDED("%lld"), (long long)entries, (long long)plan.n_apacked);
+#undef SRBCRS_NZ_PADDED
   std::vector<uint2> pairs((size_t)entries);
   parallel_for(n_groups, [&](int64_t lo, int64_t hi) {
     for (int64_t g = lo; g < hi; ++g)
