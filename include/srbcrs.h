@@ -271,7 +271,8 @@ int srbcrs_plan_trim(srbcrs_plan *plan, void *stream);
  *                below 2^24; a matrix whose stream would be mostly
  *                padding (a row with far more values than its group's
  *                others: over 8 entries per value and 2^22 entries) is
- *                refused.  C[r, :] is the sum of fl(v * B[c, :]) over
+ *                refused, before the stream is built when the groups'
+ *                lower bounds already pass that size.  C[r, :] is the sum of fl(v * B[c, :]) over
  *                the row's stored values in ascending column order, each
  *                product rounded before it is added (the fp32 CSR product,
  *                not the MFMA kernels' bits).  The first run per setting
