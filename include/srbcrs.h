@@ -287,7 +287,16 @@ int srbcrs_plan_trim(srbcrs_plan *plan, void *stream);
  *                read back in the MFMA layout; the reference's cp.async
  *                double buffer (kernel.inc:584-642) in gfx950 form.  LDS
  *                staging applies at vector width 4 (tile_b 64 and 16-byte
- *                aligned B, ldb % 4 == 0); other launches use registers.
+ *                aligned B, ldb % 4 == 0); other launches use registers;
+ *   epilogue     SRBCRS_EPILOGUE_NONE (0) or SRBCRS_EPILOGUE_RELU (1): the
+ *                kernel that writes an output value applies relu to it
+ *                (x < 0 -> +0; NaN and zeros unchanged), on every grid
+ *                order and schedule (on split schedules in the segment
+ *                reduction, not on the partial tiles); rows a packing
+ *                leaves out stay 0.  No counterpart in the reference's
+ *                SpMM: it fuses the GCN's relu(A (X W1)) into the SpMM's
+ *                store.  Not a launch knob: a tuned setting (all other
+ *                fields 0) runs with it.
  * Values outside these sets are rejected.  Every MFMA setting (grid orders
  * 0-4) yields the same bits: the per-element accumulation order does not
  * depend on them; the nonzero sweep (grid order 5) yields the fp32 CSR
@@ -300,6 +309,7 @@ typedef struct srbcrs_run_opts {
   int32_t windows_per_wave;
   int32_t a_operand;
   int32_t b_stage;
+  int32_t epilogue;
 } srbcrs_run_opts;
 
 /* a_operand: where the kernel reads the block values from.  Both give the
@@ -323,6 +333,9 @@ typedef struct srbcrs_run_opts {
 #define SRBCRS_GRID_CHUNK_SWEEP 3
 #define SRBCRS_GRID_MERGED 4
 #define SRBCRS_GRID_NZSWEEP 5
+
+#define SRBCRS_EPILOGUE_NONE 0
+#define SRBCRS_EPILOGUE_RELU 1
 
 /* srbcrs_run with explicit knobs (opts NULL = defaults). */
 int srbcrs_run_ex(srbcrs_plan *plan, const float *d_B, int64_t K, int64_t N, int64_t ldb,

@@ -172,8 +172,9 @@ class Plan:
 
     def run(self, dense: Tensor, out: Optional[Tensor] = None, depth: int = 0, tile_b: int = 0, wg_cols: int = 0,
             grid_order: int = 0, windows_per_wave: int = 0, a_operand: str = "default",
-            b_stage: str = "default") -> Tensor:
-        """out[:num_nodes] = A @ dense on the current stream.  The keyword
+            b_stage: str = "default", relu: bool = False) -> Tensor:
+        """out[:num_nodes] = A @ dense (relu(A @ dense) with relu=True, applied
+        in the kernels' stores) on the current stream.  The keyword
         knobs are the kernel template parameters (srbcrs_run_opts; 0 =
         default; grid_order 1 = chunk-major, 2 = window-major, 3 = chunk sweep, 4 = merged
         windows ("row" schedule: windows_per_wave windows interleaved per wave), 5 = nonzero
@@ -183,7 +184,8 @@ class Plan:
         "registers" / "lds" where the ring holds the gathered B rows)."""
         out = self._operands(dense, out)
         opts = _capi.RunOpts(int(depth), int(tile_b), int(wg_cols), int(grid_order), int(windows_per_wave),
-                             _capi.A_OPERANDS[a_operand], _capi.B_STAGES[b_stage])
+                             _capi.A_OPERANDS[a_operand], _capi.B_STAGES[b_stage],
+                             _capi.EPILOGUE_RELU if relu else _capi.EPILOGUE_NONE)
         with torch.cuda.device(self.device):
             _capi.check(_capi.lib().srbcrs_run_ex(self._h, dense.data_ptr(), int(dense.shape[0]), int(dense.shape[1]),
                                                   int(dense.stride(0)), out.data_ptr(), int(out.stride(0)),

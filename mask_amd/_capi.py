@@ -87,11 +87,12 @@ DUPS = {"last": 0, "sum": 1}
 class RunOpts(ctypes.Structure):
     _fields_ = [("depth", ctypes.c_int32), ("tile_b", ctypes.c_int32), ("wg_cols", ctypes.c_int32),
                 ("grid_order", ctypes.c_int32), ("windows_per_wave", ctypes.c_int32),
-                ("a_operand", ctypes.c_int32), ("b_stage", ctypes.c_int32)]
+                ("a_operand", ctypes.c_int32), ("b_stage", ctypes.c_int32), ("epilogue", ctypes.c_int32)]
 
 
 A_OPERANDS = {"default": 0, "compact": 1, "dense": 2}
 B_STAGES = {"default": 0, "registers": 1, "lds": 2}
+EPILOGUE_NONE, EPILOGUE_RELU = 0, 1   # srbcrs_run_opts.epilogue
 
 
 class SrbcrsError(RuntimeError):

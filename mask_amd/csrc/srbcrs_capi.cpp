@@ -654,6 +654,8 @@ void create_on_device(srbcrs_plan& plan, const int32_t* rowptr, const int32_t* c
   plan.sched.policy = "row";
 }
 
+// no launch knob set (the epilogue is not a launch knob: a tuned setting
+// runs with the caller's epilogue)
 bool all_default(const srbcrs_run_opts& o) {
   return !o.depth && !o.tile_b && !o.wg_cols && !o.grid_order && !o.windows_per_wave && !o.a_operand &&
          !o.b_stage;
@@ -1287,6 +1289,7 @@ static void run_impl(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
       const auto it = plan->tuned.find(N);
       if (it != plan->tuned.end()) {
         tuned_opts = it->second;
+        tuned_opts.epilogue = opts ? opts->epilogue : SRBCRS_EPILOGUE_NONE;
         opts = &tuned_opts;
       }
     }
@@ -1315,6 +1318,8 @@ static void run_impl(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
       if (opts->b_stage < 0 || opts->b_stage > 2)
         fail(SRBCRS_EINVAL, "b_stage must be 0, 1 or 2 (got %d)", opts->b_stage);
       ro.b_lds = opts->b_stage == SRBCRS_B_LDS;
+      if (opts->epilogue != SRBCRS_EPILOGUE_NONE && opts->epilogue != SRBCRS_EPILOGUE_RELU)
+        fail(SRBCRS_EINVAL, "epilogue must be 0 (none) or 1 (relu) (got %d)", opts->epilogue);
     }
     if (!plan) fail(SRBCRS_EINVAL, "plan is NULL");
     if (opts && opts->a_operand == SRBCRS_A_COMPACT && !plan->d_awords && plan->total > 0)
@@ -1352,7 +1357,8 @@ static void run_impl(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
                        (reinterpret_cast<uintptr_t>(d_C) % (4 * vec))))
       vec /= 2;
     srbcrs::StreamArgs a{d_B, d_C, nullptr, plan->d_sidx, plan->d_val, (int)plan->packed_rows, (int)N, ldb, ldc,
-                         plan->blk_h, plan->d_rowmap, plan->d_awords, plan->d_apacked};
+                         plan->blk_h, plan->d_rowmap, plan->d_awords, plan->d_apacked,
+                         opts && opts->epilogue == SRBCRS_EPILOGUE_RELU ? 1 : 0};
     // Everything that can refuse the call, and every allocation, comes before
     // the first launch: a refused call leaves C untouched.
     const bool merged = opts && opts->grid_order == SRBCRS_GRID_MERGED;
@@ -1458,7 +1464,7 @@ static void run_impl(srbcrs_plan* plan, const float* d_B, int64_t K, int64_t N, 
     hip_check(srbcrs::launch_tasks(a, tt, vec, ro, st), "launch spmm_stream(tasks)");
     srbcrs::ReduceArgs ra{partial, d_C, plan->d_red_window, plan->d_red_slot_off,
                           (int)s.red_window.size(), plan->blk_h, (int)plan->packed_rows, (int)N, ldc,
-                          plan->d_rowmap};
+                          plan->d_rowmap, a.relu};
     hip_check(srbcrs::launch_reduce(ra, vec, st), "launch segment_reduce");
 }
 

@@ -30,6 +30,7 @@ struct StreamArgs {
   const int* rowmap = nullptr;  // packed row -> output row (null = identity); M counts packed rows
   const uint2* a_words = nullptr;   // compact A (null = read val)
   const float* a_packed = nullptr;
+  int relu = 0;     // relu epilogue on the values written to C (not on partial tiles)
 };
 
 // Merged-window operands (spmm_merged): the row schedule's windows in groups
@@ -72,6 +73,7 @@ struct ReduceArgs {
   int M, N;         // M counts packed rows
   int64_t ldc;
   const int* rowmap = nullptr;
+  int relu = 0;     // relu epilogue on the sums
 };
 
 struct CsrArgs {

@@ -29,13 +29,13 @@ hipError_t launch_reduce(const ReduceArgs& a, int vec, hipStream_t st) {
   if (blocks > 65536) blocks = 65536;
   if (vec == 4)
     hipLaunchKernelGGL(segment_reduce<4>, dim3((unsigned)blocks), dim3(256), 0, st, a.partial, a.C,
-                       a.red_window, a.red_slot_off, a.n_red, a.tile_rows, a.M, a.N, a.ldc, a.rowmap);
+                       a.red_window, a.red_slot_off, a.n_red, a.tile_rows, a.M, a.N, a.ldc, a.rowmap, a.relu);
   else if (vec == 2)
     hipLaunchKernelGGL(segment_reduce<2>, dim3((unsigned)blocks), dim3(256), 0, st, a.partial, a.C,
-                       a.red_window, a.red_slot_off, a.n_red, a.tile_rows, a.M, a.N, a.ldc, a.rowmap);
+                       a.red_window, a.red_slot_off, a.n_red, a.tile_rows, a.M, a.N, a.ldc, a.rowmap, a.relu);
   else
     hipLaunchKernelGGL(segment_reduce<1>, dim3((unsigned)blocks), dim3(256), 0, st, a.partial, a.C,
-                       a.red_window, a.red_slot_off, a.n_red, a.tile_rows, a.M, a.N, a.ldc, a.rowmap);
+                       a.red_window, a.red_slot_off, a.n_red, a.tile_rows, a.M, a.N, a.ldc, a.rowmap, a.relu);
   return hipGetLastError();
 }
 

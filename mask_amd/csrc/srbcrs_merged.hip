@@ -32,7 +32,7 @@ static hipError_t launch_merged_t(const MergedArgs& m, const StreamArgs& a, hipS
   if (nwg > INT32_MAX) return hipErrorInvalidConfiguration;
   hipLaunchKernelGGL((spmm_merged<4, G, W, DEPTH, CompactA>), dim3((unsigned)nwg), dim3(64), 0, st, m.moff, m.Mo,
                      m.sidx, CompactA{m.words, a.a_packed}, a.B, a.C, a.rowmap, a.M, a.N, a.ldb, a.ldc, n_chunks,
-                     n_groups);
+                     n_groups, a.relu);
   return hipGetLastError();
 }
 

@@ -108,7 +108,7 @@ template <int VEC, int G, int W, int DEPTH, class AF>
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void spmm_merged(
     const int* __restrict__ moff, int Mo, const int* __restrict__ sidx, AF asrc, const float* __restrict__ B,
     float* __restrict__ C, const int* __restrict__ rowmap, int M, int N, int64_t ldb, int64_t ldc, int n_chunks,
-    int64_t n_groups) {
+    int64_t n_groups, int relu) {
   static_assert(W % DEPTH == 0, "the ring depth divides the round");
   constexpr int BH = 16, BW = 8;
   constexpr int WCOLS = 16 * VEC * G;
@@ -185,7 +185,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void sp
   }
 #pragma unroll
   for (int w = 0; w < W; ++w)
-    if (w < nw) store_tile<VEC, G>(acc[w][0], C, (int64_t)(w0 + w) * BH, M, ldc, col0, lane, rowmap);
+    if (w < nw) store_tile<VEC, G>(acc[w][0], C, (int64_t)(w0 + w) * BH, M, ldc, col0, lane, rowmap, relu != 0);
 }
 
 }  // namespace srbcrs

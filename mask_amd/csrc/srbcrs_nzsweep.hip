@@ -23,7 +23,7 @@ static hipError_t launch_nz_t(const NzArgs& z, const StreamArgs& a, hipStream_t 
   if (nwg == 0) return hipSuccess;
   if (nwg > INT32_MAX) return hipErrorInvalidConfiguration;
   hipLaunchKernelGGL((spmm_nzsweep<W, U, D>), dim3((unsigned)nwg), dim3(64), 0, st, z.eoff, z.pairs, a.B, a.C,
-                     a.rowmap, a.M, a.N, a.ldb, a.ldc, n_chunks, n_groups);
+                     a.rowmap, a.M, a.N, a.ldb, a.ldc, n_chunks, n_groups, a.relu);
   return hipGetLastError();
 }
 

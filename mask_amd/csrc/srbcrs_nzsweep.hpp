@@ -97,7 +97,7 @@ template <int W, int U, int D>
 __global__ __launch_bounds__(64) void spmm_nzsweep(const int* __restrict__ eoff, const uint2* __restrict__ pairs,
                                                    const float* __restrict__ B, float* __restrict__ C,
                                                    const int* __restrict__ rowmap, int M, int N, int64_t ldb,
-                                                   int64_t ldc, int n_chunks, int64_t n_groups) {
+                                                   int64_t ldc, int n_chunks, int64_t n_groups, int relu) {
   constexpr int ROWS = 16 * W;
   constexpr int Q = U / 4;   // gather instructions per sub-batch
   constexpr int P = 2 * D;   // steps per loop body
@@ -205,11 +205,12 @@ __global__ __launch_bounds__(64) void spmm_nzsweep(const int* __restrict__ eoff,
     const int64_t row = row0 + r;
     if (row < M) {
       const int64_t orow = rowmap ? rowmap[row] : row;
+      const f4 v = relu ? relu4(tile4[r * 16 + sub]) : tile4[r * 16 + sub];
 #ifdef SRBCRS_NZ_PLAIN_C_STORE
-      *reinterpret_cast<f4*>(C + orow * ldc + col0 + 4 * sub) = tile4[r * 16 + sub];
+      *reinterpret_cast<f4*>(C + orow * ldc + col0 + 4 * sub) = v;
 #else
       // C is written once: nontemporal, so that it does not push B's rows out of the L2
-      __builtin_nontemporal_store(tile4[r * 16 + sub], reinterpret_cast<f4*>(C + orow * ldc + col0 + 4 * sub));
+      __builtin_nontemporal_store(v, reinterpret_cast<f4*>(C + orow * ldc + col0 + 4 * sub));
 #endif
     }
   }

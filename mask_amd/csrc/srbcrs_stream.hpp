@@ -374,14 +374,21 @@ __device__ __forceinline__ int uniform_load(const int* __restrict__ p, int64_t i
 #endif
 }
 
+// The relu epilogue: negative values become +0; NaN, +0 and -0 pass
+// unchanged (torch.relu's results).
+__device__ __forceinline__ float relu1(float x) { return x < 0.f ? 0.f : x; }
+__device__ __forceinline__ f4 relu4(f4 v) { return f4{relu1(v[0]), relu1(v[1]), relu1(v[2]), relu1(v[3])}; }
+
 // Store a 16 x (16*VEC*G) accumulator tile.  row0 is the tile's first
 // (packed) row, rows >= row_limit are skipped (M % 16 != 0).  With a row map
 // packed row p is written to output row rowmap[p] (reordered or sparse-row
 // packings); the map is applied here, in the store, not in a separate pass.
+// relu (wave-uniform) applies the relu epilogue to the stored values.
 template <int VEC, int G>
 __device__ __forceinline__ void store_tile(const f4 (&acc)[G][VEC], float* __restrict__ out,
                                            int64_t row0, int64_t row_limit, int64_t ldc, int col0,
-                                           int lane, const int* __restrict__ rowmap = nullptr) {
+                                           int lane, const int* __restrict__ rowmap = nullptr,
+                                           bool relu = false) {
   typedef typename VecT<VEC>::type V;
   const int k = lane >> 4;
   // The tile's 16 map entries are read with scalar loads (clamped to the
@@ -419,6 +426,14 @@ __device__ __forceinline__ void store_tile(const f4 (&acc)[G][VEC], float* __res
 #pragma unroll
           for (int s = 0; s < VEC; ++s) v[s] = acc[g][s][r];
         }
+        if (relu) {
+          if constexpr (VEC == 1) {
+            v = relu1(v);
+          } else {
+#pragma unroll
+            for (int s = 0; s < VEC; ++s) v[s] = relu1(v[s]);
+          }
+        }
 #ifdef SRBCRS_EXPERIMENT_PLAIN_C_STORE
         *reinterpret_cast<V*>(p + 16 * VEC * g) = v;
 #else
@@ -440,6 +455,7 @@ struct RowTasks {
   int Mo;
   int wpw;
   const int* __restrict__ rowmap = nullptr;   // packed row -> output row (null = identity)
+  int relu = 0;                               // relu epilogue on the output rows
   __device__ __forceinline__ void group(int g, int& t0, int& t1) const {
     t0 = g * wpw;
     t1 = t0 + wpw < Mo ? t0 + wpw : Mo;
@@ -458,6 +474,7 @@ struct TableTasks {
   const int* __restrict__ task_window;
   const int* __restrict__ task_slot;
   const int* __restrict__ rowmap = nullptr;   // packed row -> output row (null = identity)
+  int relu = 0;                               // relu epilogue on rows written to C (not on partials)
   __device__ __forceinline__ void group(int g, int& t0, int& t1) const {
     t0 = uniform_load(group_off, g);
     t1 = uniform_load(group_off, g + 1);
@@ -476,7 +493,8 @@ __device__ __forceinline__ void flush_task(const Src& src, int t, f4 (&acc)[BH /
 #pragma unroll
   for (int h = 0; h < BH / 16; ++h) {
     if (slot < 0)
-      store_tile<VEC, G>(acc[h], C, (int64_t)src.window(t) * BH + 16 * h, M, ldc, col0, lane, src.rowmap);
+      store_tile<VEC, G>(acc[h], C, (int64_t)src.window(t) * BH + 16 * h, M, ldc, col0, lane, src.rowmap,
+                         src.relu != 0);
     else
       store_tile<VEC, G>(acc[h], partial, (int64_t)slot * BH + 16 * h, (int64_t)(slot + 1) * BH, ldc,
                          col0, lane);
@@ -705,14 +723,15 @@ __global__ __launch_bounds__(64 * WAVES) void spmm_stream(
 // counterpart of the reference's reduce_tcf_segments
 // (examples/src_fp32/acc/testbed/custom_format_e2e.cu:832-853).  One thread
 // per VEC consecutive columns.  M counts packed rows; rowmap (or null) maps
-// them to output rows as in store_tile.
+// them to output rows as in store_tile; relu applies the relu epilogue to
+// the sums.
 template <int VEC>
 __global__ __launch_bounds__(256) void segment_reduce(const float* __restrict__ partial,
                                                       float* __restrict__ C,
                                                       const int* __restrict__ red_window,
                                                       const int* __restrict__ red_slot_off,
                                                       int n_red, int tile_rows, int M, int N,
-                                                      int64_t ldc, const int* __restrict__ rowmap) {
+                                                      int64_t ldc, const int* __restrict__ rowmap, int relu) {
   typedef typename VecT<VEC>::type V;
   const int64_t nv = N / VEC;
   const int64_t per = tile_rows * nv;
@@ -729,6 +748,9 @@ __global__ __launch_bounds__(256) void segment_reduce(const float* __restrict__ 
     if constexpr (VEC == 1) s = 0.f; else { for (int q = 0; q < VEC; ++q) s[q] = 0.f; }
     for (int sl = red_slot_off[i]; sl < red_slot_off[i + 1]; ++sl)
       s += *reinterpret_cast<const V*>(partial + ((int64_t)sl * tile_rows + r) * ldc + VEC * cv);
+    if (relu) {
+      if constexpr (VEC == 1) s = relu1(s); else { for (int q = 0; q < VEC; ++q) s[q] = relu1(s[q]); }
+    }
     const int64_t orow = rowmap ? (int64_t)rowmap[row] : row;
     *reinterpret_cast<V*>(C + orow * ldc + VEC * cv) = s;
   }

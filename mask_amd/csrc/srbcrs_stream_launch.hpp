@@ -90,14 +90,14 @@ template <class AF>
 static hipError_t launch_row_af(const AF& af, const StreamArgs& a, const int* soff, int Mo, int vec,
                                 const RunOpts& o, hipStream_t st) {
   const int wpw = o.windows_per_wave > 0 ? o.windows_per_wave : 1;
-  RowTasks src{soff, Mo, wpw, a.rowmap};
+  RowTasks src{soff, Mo, wpw, a.rowmap, a.relu};
   return launch_src(src, af, (Mo + wpw - 1) / wpw, a, vec, o, st);
 }
 
 template <class AF>
 static hipError_t launch_tasks_af(const AF& af, const StreamArgs& a, const TaskTable& t, int vec,
                                   const RunOpts& o, hipStream_t st) {
-  TableTasks src{t.group_off, t.task_begin, t.task_end, t.task_window, t.task_slot, a.rowmap};
+  TableTasks src{t.group_off, t.task_begin, t.task_end, t.task_window, t.task_slot, a.rowmap, a.relu};
   return launch_src(src, af, t.n_groups, a, vec, o, st);
 }
 

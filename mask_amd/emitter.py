@@ -325,7 +325,7 @@ extern "C" int sparsene_generated_reduce(const float* partial, float* C, const i
   if (blocks > 65536) blocks = 65536;
   hipLaunchKernelGGL(srbcrs::segment_reduce<kVEC>, dim3((unsigned)blocks), dim3(256), 0,
                      static_cast<hipStream_t>(stream), partial, C, red_window, red_slot_off, n_red, kBH,
-                     M, N, (int64_t)ldc, rowmap);
+                     M, N, (int64_t)ldc, rowmap, 0);
   return hipGetLastError() == hipSuccess ? 0 : -2;
 }}
 
