@@ -122,6 +122,21 @@ int main(void) {
     CHECK(srbcrs_run(plan, dB, K, N, N, dC, N, M, NULL));
     HIPCHECK(hipMemcpy(C, dC, sizeof(float) * M * N, hipMemcpyDeviceToHost));
     if (check(C, rp, ci, v, B, M, N)) return 1;
+    /* the relu epilogue on the tuned setting: relu of the plain output, bit for bit */
+    {
+      srbcrs_run_opts relu = {0};
+      relu.epilogue = SRBCRS_EPILOGUE_RELU;
+      float* R = (float*)malloc(sizeof(float) * M * N);
+      HIPCHECK(hipMemset(dC, 0, sizeof(float) * M * N));
+      CHECK(srbcrs_run_ex(plan, dB, K, N, N, dC, N, M, &relu, NULL));
+      HIPCHECK(hipMemcpy(R, dC, sizeof(float) * M * N, hipMemcpyDeviceToHost));
+      for (size_t i = 0; i < (size_t)M * N; ++i)
+        if (R[i] != (C[i] < 0.f ? 0.f : C[i])) {
+          fprintf(stderr, "relu epilogue mismatch at %zu: %g vs %g\n", i, R[i], C[i]);
+          return 1;
+        }
+      free(R);
+    }
     /* an error path: N not a multiple of 16 */
     if (srbcrs_run(plan, dB, K, 24, N, dC, N, M, NULL) != SRBCRS_EINVAL) {
       fprintf(stderr, "expected SRBCRS_EINVAL\n");
