@@ -172,6 +172,32 @@ def test_full_size_gcn_two_layer_forward(gpu):
         E.reset_backend_state()
 
 
+def test_full_size_gcn_relu_epilogue(gpu):
+    """The GCN forward's first SpMM at full size with the relu epilogue (split
+    schedule, the bench's published setting): torch.relu of the plain output,
+    bit for bit, and the fp64 oracle gate of relu(A X W1) on a row sample."""
+    import torch
+    import bench
+    from mask_amd.SRBCRSSpMM import Plan
+    m = _workload("gcn-232965")
+    _say("full gcn relu epilogue", m.M, m.nnz)
+    dev = torch.device("cuda", 0)
+    t = lambda a: torch.from_numpy(a).to(dev)
+    plan = Plan(t(m.rowptr), t(m.colind), t(m.values), m.M)
+    plan.set_schedule("split", 0)
+    knobs = {k: v for k, v in bench.PUBLISHED_KNOBS["gcn-232965"].items() if k != "N"}
+    X = torch.from_numpy(np.random.default_rng(m.seed).uniform(-1, 1, (m.K, 256)).astype(np.float32)).to(dev)
+    plain = plan.run(X, **knobs)
+    fused = plan.run(X, relu=True, **knobs)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, torch.relu(plain))
+    rows = np.sort(np.random.default_rng(6).choice(m.M, 3000, replace=False))
+    rp, ci, vv = _rows_csr(m, rows)
+    ref, scale = oracle.csr_spmm_f64(rp, ci, vv, X.cpu().numpy(), rows.size, with_abs=True)
+    met = oracle.error_metrics(fused.cpu().numpy()[rows], np.maximum(ref, 0), scale)
+    assert met["max_ratio"] <= TOL_ELEM and met["ref_gate"] and met["rel_l2"] <= 1e-6, met
+
+
 @pytest.mark.parametrize("name", ["uniform-65536", "banded-524288", "rmat-2^20", "gcn-232965"])
 def test_full_size_integer_protocol_exact(gpu, name):
     """Every output element at full size, without a tolerance: the reference
