@@ -375,6 +375,49 @@ def test_header_is_c99_and_c_client_builds(tmp_path):
     assert compile_client(tmp_path / "client").exists()
 
 
+def test_ctypes_structs_and_constants_match_the_header(tmp_path):
+    """The ctypes mirrors of the ABI's structs have the C layout (size and
+    every field's offset, from a C99 program compiled against
+    include/srbcrs.h) and the constants the Python side passes equal the
+    header's #defines: a field added to one side only fails here."""
+    import subprocess
+    structs = {"srbcrs_plan_desc": _capi.PlanDesc, "srbcrs_pack_opts": _capi.PackOpts,
+               "srbcrs_run_opts": _capi.RunOpts}
+    lines = ['#include <stddef.h>', '#include <stdio.h>', '#include "srbcrs.h"', "int main(void) {"]
+    for cname, py in structs.items():
+        lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
+        for f, _ in py._fields_:
+            lines.append(f'  printf("{cname} {f} %zu\\n", offsetof({cname}, {f}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", f"-I{ROOT / 'include'}", str(src), "-o", str(exe)],
+                   check=True)
+    got = dict(l.rsplit(" ", 1) for l in subprocess.run([str(exe)], check=True, capture_output=True,
+                                                        text=True).stdout.splitlines())
+    for cname, py in structs.items():
+        assert int(got[f"{cname} size"]) == ctypes.sizeof(py), cname
+        for f, _ in py._fields_:
+            assert int(got[f"{cname} {f}"]) == getattr(py, f).offset, (cname, f)
+    text = (ROOT / "include" / "srbcrs.h").read_text()
+    defs = {k: int(v) for k, v in re.findall(r"#define (SRBCRS_[A-Z_0-9]+) \(?(-?\d+)\)?", text)}
+    assert defs["SRBCRS_OK"] == _capi.SRBCRS_OK and defs["SRBCRS_EINVAL"] == _capi.SRBCRS_EINVAL
+    assert defs["SRBCRS_ESTATE"] == _capi.SRBCRS_ESTATE and defs["SRBCRS_ENOMEM"] == _capi.SRBCRS_ENOMEM
+    assert defs["SRBCRS_TUNE_NONZERO_SWEEP"] == _capi.SRBCRS_TUNE_NONZERO_SWEEP
+    assert (defs["SRBCRS_EPILOGUE_NONE"], defs["SRBCRS_EPILOGUE_RELU"]) == (_capi.EPILOGUE_NONE, _capi.EPILOGUE_RELU)
+    for k, v in _capi.A_OPERANDS.items():
+        assert defs[f"SRBCRS_A_{k.upper()}"] == v
+    for k, v in _capi.B_STAGES.items():
+        assert defs[f"SRBCRS_B_{k.upper()}"] == v
+    assert defs["SRBCRS_PACK_CONDENSED"] == _capi.PACKINGS["column_condensed_dense"]
+    assert defs["SRBCRS_PACK_FIXED_BLOCKS"] == _capi.PACKINGS["active_fixed_blocks_dense"]
+    assert (defs["SRBCRS_DUP_LAST"], defs["SRBCRS_DUP_SUM"]) == (_capi.DUPS["last"], _capi.DUPS["sum"])
+    for name, hdr in (("identity", "IDENTITY"), ("row_rcm", "RCM"), ("first_col_sort", "FIRST_COL"),
+                      ("jaccard_greedy", "JACCARD"), ("sparse_rows", "SPARSE_ROWS"), ("explicit", "EXPLICIT")):
+        assert defs[f"SRBCRS_ORDER_{hdr}"] == _capi.ORDERS[name], name
+
+
 @pytest.mark.parametrize("n_shards", [1, 2, 3, 8, 50])
 def test_shard_windows_balanced_and_contiguous(n_shards):
     """Contiguous cover of the windows; each shard's cost (blocks + 1 per
